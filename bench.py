@@ -1,0 +1,196 @@
+#!/usr/bin/env python3
+"""Benchmark: integer event-by-event forward (salt_core/quant semantics) on one MI355X.
+
+Default workload: the N-MNIST-shaped network of the benchmark configuration 3 (conv
+2->16 5x5 s2 -> conv 16->32 3x3 s2 -> FC 1568->10, 1024 synthetic streams of ~4500
+events).  A step = one forward of the whole network over the batch, inputs resident in
+HBM, every layer's spike stream, final registers and per-stream statistics written.
+
+Prints one JSON line (the driver's contract).  value = layer-1 input events / second.
+The step's output is checked bit for bit against the CPU oracle, whose timing on the
+host cores is the cpu_baseline.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "spiking-affine-lazy-training_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "input events/sec (batch, 1 MI355X) bit-exact vs salt_core/quant; % HBM/LDS roofline"
+HBM_PEAK_GBS = 8000.0                     # MI355X HBM3E
+LDS_PEAK_GBS = 256 * 128 * 2.4            # 256 CUs x 128 B/clk x 2.4 GHz = 78.6 TB/s
+
+
+def conv_update_counts(layer, src, n_real):
+    """Per stream, the number of (neuron, event) register updates of a conv layer: the
+    valid candidate positions of every real event x output channels (numpy, host)."""
+    import numpy as np
+    K, S, P = layer.k, layer.s, layer.p
+    hw = layer.h_in * layer.w_in
+    L = src.shape[1]
+    real = np.arange(L)[None, :] < n_real[:, None]
+    rem = src % hw
+    y, x = rem // layer.w_in, rem % layer.w_in
+
+    def axis(i, o_max):
+        lo = np.maximum(-((-(i + P - K + 1)) // S), 0)
+        hi = np.minimum((i + P) // S, o_max - 1)
+        return np.maximum(hi - lo + 1, 0)
+
+    per_event = axis(y, layer.h_out) * axis(x, layer.w_out) * layer.oc
+    return (per_event * real).sum(axis=1)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3, help="benchmark configuration 1..5")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (0: all, max 16)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the check")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(streams would shard across GPUs with no communication; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from salt_amd import workloads as W
+    from salt_amd.runner import NetworkRunner
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    w = W.CONFIGS[args.config]()
+    net = w.network
+    runner = NetworkRunner(net, w.params, w.round_mode, dev)
+    stream = net.input_stream(w.events, device=dev)
+    n_events = int(w.events.n_real_events.sum())
+    B, L = w.events.event_times.shape
+    n_layers = len(net.layers)
+
+    for _ in range(max(args.warmup, 1)):
+        outs = runner.run(stream)
+    torch.cuda.synchronize()
+    fits = runner.check_fits(outs)
+
+    # Timed region: K steps bracketed by synchronize; per-layer HIP events on the stream
+    # the kernels are launched on (torch's current stream).
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n_layers)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    from salt_amd.quant.backend import run_layer_kernel
+    for k in range(args.steps):
+        times, src, n_real = stream.event_times, stream.event_source_idx, stream.n_real_events
+        outs = []
+        for i, (layer, dp) in enumerate(zip(net.layers, runner.dev_params)):
+            ev[k][i][0].record()
+            o = run_layer_kernel(layer, dp, runner.round_mode, times, src, n_real,
+                                 int(layer.max_out_spikes), extremes=False,
+                                 fill_pads=(i == n_layers - 1))
+            ev[k][i][1].record()
+            outs.append(o)
+            times, src, n_real = o.times, o.src, o.n
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    layer_ms = np.array([[ev[k][i][0].elapsed_time(ev[k][i][1]) for i in range(n_layers)]
+                         for k in range(args.steps)]).mean(axis=0)
+    ms_per_step = wall * 1000.0 / args.steps
+    value = n_events / (ms_per_step / 1000.0)
+
+    # Algorithmic traffic of each layer (per launch): LDS = updates x (4 + 4 + weight bytes),
+    # HBM = 8 B per input event + 8 B per spike + 4 B per final register + weights.
+    host = [(o.src.cpu().numpy(), o.n.cpu().numpy()) for o in outs]
+    in_src, in_n = w.events.source_idx, w.events.n_real_events
+    per_layer = []
+    for i, (layer, p, dp) in enumerate(zip(net.layers, w.params, runner.dev_params)):
+        wbytes = dp.q_bits // 8
+        n_in_events = int(np.minimum(in_n, in_src.shape[1]).sum())
+        if hasattr(layer, "oc"):
+            updates = int(conv_update_counts(layer, in_src, np.minimum(in_n, in_src.shape[1])).sum())
+        else:
+            updates = n_in_events * layer.n_out
+        spikes = int(host[i][1].sum())
+        lds = updates * (8 + wbytes)
+        hbm = 8 * n_in_events + 8 * spikes + 4 * B * layer.n_neurons + dp.q.numel() * wbytes
+        per_layer.append(dict(name=layer.name, ms=float(layer_ms[i]), updates=updates,
+                              spikes=spikes, lds_bytes=lds, hbm_bytes=hbm))
+        in_src, in_n = host[i]
+    dom = max(per_layer, key=lambda d: d["ms"])
+    lds_gbs = dom["lds_bytes"] / (dom["ms"] * 1e-3) / 1e9
+    hbm_gbs = dom["hbm_bytes"] / (dom["ms"] * 1e-3) / 1e9
+    lds_frac, hbm_frac = lds_gbs / LDS_PEAK_GBS, hbm_gbs / HBM_PEAK_GBS
+    bound = "lds" if lds_frac >= hbm_frac else "hbm"
+    roofline = {"bound": bound, "kernel": dom["name"],
+                "achieved": round(lds_gbs if bound == "lds" else hbm_gbs, 2),
+                "peak": LDS_PEAK_GBS if bound == "lds" else HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(lds_frac if bound == "lds" else hbm_frac, 5),
+                "traffic": None,
+                "hbm": {"achieved": round(hbm_gbs, 2), "peak": HBM_PEAK_GBS, "frac": round(hbm_frac, 6)},
+                "lds": {"achieved": round(lds_gbs, 2), "peak": LDS_PEAK_GBS, "frac": round(lds_frac, 5)},
+                "layers": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
+                           for d in per_layer]}
+
+    cpu = None
+    bit_exact = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
+        specs = []
+        for layer, p in zip(net.layers, w.params):
+            if hasattr(layer, "oc"):
+                g = dict(kind="conv", ic=layer.ic, h_in=layer.h_in, w_in=layer.w_in, oc=layer.oc,
+                         k=layer.k, s=layer.s, p=layer.p, max_queue_len=layer.max_queue_len)
+            else:
+                g = dict(kind="fc", n_in=layer.n_in, n_out=layer.n_out)
+            specs.append((g, dict(q=p.q, table=p.decay_table_int, v_th=p.v_th_int, f_a=p.f_a,
+                                  f_V=p.f_V, i_V=p.i_V, round_mode=w.round_mode,
+                                  overflow_mode=p.overflow_mode), layer.max_out_spikes))
+        t_c = time.perf_counter()
+        ref = O.network_forward(specs, *w.events, nthreads=threads)
+        cpu_s = time.perf_counter() - t_c
+        cpu = {"value": round(n_events / cpu_s, 1), "unit": "input events/s", "cores": threads,
+               "kind": "port",
+               "sample": f"the full workload ({B} streams, {n_events} events), oracle/salt_oracle.c "
+                         f"-O3, OpenMP over streams, {cpu_s:.2f} s"}
+        bit_exact = True
+        for o, r in zip(outs, ref):
+            ok = (np.array_equal(o.n.cpu().numpy(), r["out_n"])
+                  and np.array_equal(o.v_final.cpu().numpy(), r["v_final"])
+                  and np.array_equal(o.stats[:, 0].cpu().numpy(), r["v_min"].min(axis=1))
+                  and np.array_equal(o.stats[:, 1].cpu().numpy(), r["v_max"].max(axis=1)))
+            n_max = int(r["out_n"].max())
+            ok = ok and np.array_equal(o.src[:, :n_max].cpu().numpy(), r["out_src"][:, :n_max])
+            ok = ok and np.array_equal(o.times[:, :n_max].cpu().numpy(), r["out_times"][:, :n_max])
+            bit_exact = bit_exact and bool(ok)
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "input events/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int32",
+        "data": "synthetic",
+        "config": {"workload": w.name, "streams": B, "padded_len": L, "input_events": n_events,
+                   "layers": [l.name for l in net.layers], "round_mode": w.round_mode,
+                   "f_a": 10, "f_V": 0, "i_V": 24, "overflow": "wrap"},
+        "bit_exact": bit_exact, "fits": bool(fits.all()),
+        "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if (bit_exact is not False and bool(fits.all())) else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,131 @@
+"""GPU path vs the CPU oracle, bit for bit: spike streams (times, sources, counts),
+final registers, per-neuron and per-stream extremes, needed queue lengths.  Geometries
+are chosen to exercise each work decomposition: whole layer in one wave per stream
+(direct output), channel groups and row bands (spike masks + compaction), FC slices."""
+import numpy as np
+import pytest
+
+from salt_amd import ConvLayer, FCLayer, QuantizedLayerParams
+from salt_amd.quant.codes import build_decay_table_int
+from oracle import oracle as O
+from helpers import assert_layer_equal, oracle_spec
+from gpu_util import run_layer
+
+pytestmark = pytest.mark.gpu
+
+MODES = [("round", "wrap", 10, 0, 24), ("truncate", "saturate", 6, 2, 12), ("round", "saturate", 15, 3, 27),
+         ("truncate", "wrap", 4, 1, 29), ("round", "wrap", 0, 0, 20)]
+
+
+def _events(rng, B, L, n_src, t_max=200, dup=0.25):
+    times = np.zeros((B, L), np.float32)
+    src = rng.integers(0, n_src, (B, L)).astype(np.int32)
+    n_real = rng.integers(max(1, L // 2), L + 1, B).astype(np.int32)
+    n_real[0] = L
+    if B > 1:
+        n_real[1] = 0
+    for b in range(B):
+        gaps = np.where(rng.random(L) < dup, 0, rng.integers(1, max(2, 2 * t_max // L), L))
+        times[b] = np.cumsum(gaps)
+        times[b, n_real[b]:] = 1e12
+    return times, src, n_real
+
+
+def _params(rng, shape, n_neurons, oc, mode, bits, vth_kind):
+    rm, om, fa, fV, iV = mode
+    lim = {8: 127, 16: 2000, 32: 70000}[bits]
+    q = rng.integers(-lim, lim + 1, shape)
+    tab = build_decay_table_int(fa, 12.0)
+    if tab.size == 0:
+        tab = np.zeros(1, np.int32)
+    hi = max(2, min(2 ** (iV + fV - 1) - 1, lim * (1 << fV)))
+    if vth_kind == "none":
+        vth = None
+    elif vth_kind == "scalar":
+        vth = np.int32(rng.integers(1, hi))
+    elif vth_kind == "channel":
+        vth = np.repeat(rng.integers(1, hi, oc), n_neurons // oc).astype(np.int32)
+    else:
+        vth = rng.integers(1, hi, n_neurons).astype(np.int32)
+    return QuantizedLayerParams(q=q, decay_table_int=tab, v_th_int=vth, scale=np.float32(1.0),
+                                f_a=fa, f_V=fV, i_V=iV, overflow_mode=om), rm
+
+
+CONV_CASES = [
+    # (ic, h, w, oc, k, s, p, B, L)  -- comment: expected plan
+    (2, 10, 10, 2, 3, 1, 0, 16, 200),      # direct: one wave per stream
+    (2, 12, 12, 8, 3, 1, 1, 8, 300),       # channel groups -> masks
+    (2, 34, 34, 16, 5, 2, 0, 8, 400),      # N-MNIST conv1 geometry
+    (16, 15, 15, 32, 3, 2, 0, 8, 400),     # N-MNIST conv2 geometry
+    (1, 130, 130, 4, 3, 1, 0, 4, 800),     # row bands (state above the LDS budget)
+    (3, 9, 11, 5, 4, 3, 2, 8, 150),        # odd sizes, stride 3, padding 2
+    (1, 7, 7, 3, 1, 2, 0, 8, 100),         # k < s: some pixels reach no neuron
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+@pytest.mark.parametrize("mi", range(len(MODES)))
+def test_conv_matches_oracle(case, mi):
+    ic, h, w, oc, k, s, p, B, L = case
+    rng = np.random.default_rng(1000 * mi + sum(case))
+    layer = ConvLayer(name="c", ic=ic, h_in=h, w_in=w, oc=oc, k=k, s=s, p=p, init_k=1.0,
+                      max_queue_len=int(rng.choice([L + 1, max(2, L // 20)])),
+                      max_out_spikes=int(rng.choice([4 * L * oc, 7])))
+    bits = [8, 16, 32][mi % 3]
+    vk = ["scalar", "channel", "neuron", "none"][mi % 4]
+    params, rm = _params(rng, layer.weight_shape, layer.n_neurons, oc, MODES[mi], bits, vk)
+    times, src, n_real = _events(rng, B, L, ic * h * w)
+    print("conv case", case, "mode", MODES[mi], "bits", bits, "vth", vk, "mql", layer.max_queue_len,
+          "cap", layer.max_out_spikes, flush=True)
+    out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+    geom, prm, cap = oracle_spec(layer, params, rm)
+    ref = O.layer_forward(geom, prm, times, src, n_real, cap)
+    assert_layer_equal(out, ref, tag=str(case))
+
+
+FC_CASES = [(2312, 128, 4, 300), (37, 10, 16, 200), (100, 1000, 4, 120), (64, 1500, 3, 80), (5, 1, 8, 50)]
+
+
+@pytest.mark.parametrize("case", FC_CASES)
+@pytest.mark.parametrize("mi", range(len(MODES)))
+def test_fc_matches_oracle(case, mi):
+    n_in, n_out, B, L = case
+    rng = np.random.default_rng(7 + 100 * mi + n_out)
+    layer = FCLayer(name="f", n_in=n_in, n_out=n_out, init_k=1.0,
+                    max_out_spikes=int(rng.choice([L * n_out, 5])))
+    bits = [8, 16, 32][mi % 3]
+    vk = ["scalar", "channel", "none"][mi % 3]
+    params, rm = _params(rng, layer.weight_shape, n_out, n_out, MODES[mi], bits, vk)
+    times, src, n_real = _events(rng, B, L, n_in)
+    print("fc case", case, "mode", MODES[mi], "bits", bits, "vth", vk, flush=True)
+    out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+    geom, prm, cap = oracle_spec(layer, params, rm)
+    ref = O.layer_forward(geom, prm, times, src, n_real, cap)
+    assert_layer_equal(out, ref, tag=str(case))
+
+
+def test_without_neuron_extremes_same_streams_and_registers():
+    rng = np.random.default_rng(5)
+    layer = ConvLayer(name="c", ic=2, h_in=34, w_in=34, oc=16, k=5, s=2, p=0, init_k=1.0,
+                      max_queue_len=500, max_out_spikes=4000)
+    params, rm = _params(rng, layer.weight_shape, layer.n_neurons, 16, MODES[0], 8, "scalar")
+    times, src, n_real = _events(rng, 8, 400, 2 * 34 * 34)
+    a = run_layer(layer, params, times, src, n_real, round_mode=rm, extremes=True)
+    b = run_layer(layer, params, times, src, n_real, round_mode=rm, extremes=False)
+    assert b.result.v_unfitted_min is None
+    for x, y in [(a.stream.event_times, b.stream.event_times), (a.stream.event_source_idx, b.stream.event_source_idx),
+                 (a.result.v_final, b.result.v_final), (a.result.stream_stats, b.result.stream_stats)]:
+        assert bool((x == y).all())
+
+
+def test_repeat_runs_are_bitwise_identical():
+    """Determinism: spike order never depends on atomics or scheduling."""
+    rng = np.random.default_rng(9)
+    layer = ConvLayer(name="c", ic=1, h_in=130, w_in=130, oc=4, k=3, s=1, p=0, init_k=1.0,
+                      max_queue_len=900, max_out_spikes=20000)
+    params, rm = _params(rng, layer.weight_shape, layer.n_neurons, 4, MODES[0], 8, "scalar")
+    times, src, n_real = _events(rng, 4, 800, 130 * 130)
+    a = run_layer(layer, params, times, src, n_real, round_mode=rm)
+    b = run_layer(layer, params, times, src, n_real, round_mode=rm)
+    assert bool((a.stream.event_source_idx == b.stream.event_source_idx).all())
+    assert bool((a.result.v_final == b.result.v_final).all())
