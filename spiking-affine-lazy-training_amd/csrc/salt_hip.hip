@@ -136,11 +136,6 @@ __device__ __forceinline__ float rdlanef(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-template <typename T>
-__device__ __forceinline__ int32_t load_code(const void* p, size_t i) {
-  return (int32_t)static_cast<const T*>(p)[i];
-}
-
 // Extended decay table: [0] = 2^f_a (identity), [1..n] = table, [n+1] = 0.
 __device__ void load_ext_table(int32_t* ext, const int32_t* table, int n_table, int fa,
                                int lane) {
@@ -170,6 +165,7 @@ struct ConvArgs {
   Quant qz;
   const int32_t* table;
   const void* q;
+  int q_bits;
   // events
   int L;
   const float* times;
@@ -187,9 +183,39 @@ struct ConvArgs {
   uint32_t* masks;
 };
 
-// LDS layout (int32 words): ext[n_table+2] | qs[G*IC*K*K] | V[G*R*W] | tl[R*W] |
-// cnt[R*W] | (EXT) mn[G*R*W] | mx[G*R*W]
-template <typename QT, bool FAST24, bool EXT>
+__device__ __forceinline__ int32_t load_code_bits(const void* p, size_t i, int bits) {
+  if (bits == 8) return (int32_t) static_cast<const int8_t*>(p)[i];
+  if (bits == 16) return (int32_t) static_cast<const int16_t*>(p)[i];
+  return static_cast<const int32_t*>(p)[i];
+}
+
+template <typename T>
+__device__ __forceinline__ T lds_at(char* base, int byte_off) {
+  return *reinterpret_cast<T*>(base + byte_off);
+}
+template <typename T>
+__device__ __forceinline__ void lds_put(char* base, int byte_off, T v) {
+  *reinterpret_cast<T*>(base + byte_off) = v;
+}
+
+// LDS layout (4-byte words): trash[64] | ext[n_table+2] | vthc[G] | qs[G*IC*K*K] |
+// V[G*R*W] | tl[R*W] | cnt[R*W] | (EXT) mn[G*R*W] | mx[G*R*W] | (VTHN) th[G*R*W]
+constexpr int kConvFixedWords = 64;
+
+size_t conv_lds_words(int n_table, int G, int IC, int K, int R, int W, bool ext, bool vthn) {
+  return (size_t)kConvFixedWords + (size_t)(n_table + 2) + (size_t)G +
+         (size_t)G * IC * K * K + (size_t)G * R * W * (1 + (ext ? 2 : 0) + (vthn ? 1 : 0)) +
+         2 * (size_t)R * W;
+}
+
+// One wave per (stream, partition).  Per event, the updates are the valid candidate
+// rectangle (ny x nx positions) times the partition's channels, compacted onto lanes:
+// item u -> channel u / (ny*nx), position u % (ny*nx) (exact float-reciprocal division).
+// The iteration body has no divergent branches: lanes without an update read from a
+// safe address and write to their own trash word.  All LDS reads of an event are
+// issued before their results are needed (two dependent round trips: registers, codes,
+// last times, counts, then decay codes).  NIT bounds the iterations per event.
+template <bool FAST24, bool EXT, bool VTHN, int NIT>
 __global__ void __launch_bounds__(64) conv_layer_kernel(ConvArgs a) {
   extern __shared__ int32_t smem[];
   const int lane = threadIdx.x;
@@ -200,24 +226,33 @@ __global__ void __launch_bounds__(64) conv_layer_kernel(ConvArgs a) {
   const int ocn = min(a.G, a.OC - oc0);
   const int r0 = rb * a.R;
   const int rn = min(a.R, a.H - r0);
-  const int PW = rn * a.W;  // positions in this partition
+  const int W = a.W;
+  const int PW = rn * W;  // positions in this partition
   const int KK = a.K * a.K;
   const Quant& qz = a.qz;
 
-  int32_t* ext = smem;
-  int32_t* qs = ext + (qz.n_table + 2);
+  int32_t* ext = smem + kConvFixedWords;
+  int32_t* vthc = ext + (qz.n_table + 2);
+  int32_t* qs = vthc + a.G;
   int32_t* Vs = qs + a.G * a.IC * KK;
-  float* tl = reinterpret_cast<float*>(Vs + a.G * a.R * a.W);
-  int32_t* cnt = reinterpret_cast<int32_t*>(tl + a.R * a.W);
-  int32_t* mn = cnt + a.R * a.W;
-  int32_t* mx = mn + a.G * a.R * a.W;
+  float* tl = reinterpret_cast<float*>(Vs + a.G * a.R * W);
+  int32_t* cnt = reinterpret_cast<int32_t*>(tl + a.R * W);
+  int32_t* mn = cnt + a.R * W;
+  int32_t* mx = mn + (EXT ? a.G * a.R * W : 0);
+  int32_t* th = mx + (EXT ? a.G * a.R * W : 0);
 
   load_ext_table(ext, a.table, qz.n_table, qz.fa, lane);
+  for (int i = lane; i < a.G; i += kWave)
+    vthc[i] = qz.vth_kind == SALT_VTH_PER_CHANNEL ? qz.vth[min(oc0 + i, a.OC - 1)] : qz.vth_scalar;
   for (int i = lane; i < ocn * a.IC * KK; i += kWave)
-    qs[i] = load_code<QT>(a.q, (size_t)oc0 * a.IC * KK + i);
+    qs[i] = load_code_bits(a.q, (size_t)oc0 * a.IC * KK + i, a.q_bits);
   for (int i = lane; i < ocn * PW; i += kWave) {
     Vs[i] = 0;
     if (EXT) { mn[i] = 0; mx[i] = 0; }
+    if (VTHN) {
+      const int ocl = i / PW;
+      th[i] = qz.vth[(oc0 + ocl) * a.HW + r0 * W + (i - ocl * PW)];
+    }
   }
   for (int i = lane; i < PW; i += kWave) { tl[i] = 0.0f; cnt[i] = 0; }
   __syncthreads();
@@ -228,28 +263,24 @@ __global__ void __launch_bounds__(64) conv_layer_kernel(ConvArgs a) {
   const float* tb = a.times + (size_t)b * L;
   const int32_t* sb = a.src + (size_t)b * L;
   const bool has_vth = qz.vth_kind != SALT_VTH_NONE;
+  const float tab_top = (float)(qz.n_table + 1);
+  const uint32_t qfV = (uint32_t)qz.fV;
 
-  // Per-lane constants of the update items u = it*64 + lane -> (channel, dy, dx).
-  const int n_items = ocn * a.NC2;
-  const int nit = (n_items + kWave - 1) / kWave;
-  int it_oc[kMaxIt], it_r[kMaxIt], it_qoff[kMaxIt], it_vth[kMaxIt];
-  bool it_ok[kMaxIt];
+  char* const lds = reinterpret_cast<char*>(smem);
+  const int trash4 = lane * 4;  // this lane's trash word
+  const int ext4 = (int)(reinterpret_cast<char*>(ext) - lds);
+  const int vthc4 = (int)(reinterpret_cast<char*>(vthc) - lds);
+  const int qs4 = (int)(reinterpret_cast<char*>(qs) - lds);
+  const int vs4 = (int)(reinterpret_cast<char*>(Vs) - lds);
+  const int tl4 = (int)(reinterpret_cast<char*>(tl) - lds);
+  const int cnt4 = (int)(reinterpret_cast<char*>(cnt) - lds);
+  const int mn4 = (int)(reinterpret_cast<char*>(mn) - lds);
+  const int mx4 = (int)(reinterpret_cast<char*>(mx) - lds);
+  const int th4 = (int)(reinterpret_cast<char*>(th) - lds);
+  const int PW4 = PW * 4, ICKK4 = a.IC * KK * 4, SK4 = a.S * a.K * 4, S4 = a.S * 4;
+  float uf[NIT];
 #pragma unroll
-  for (int it = 0; it < kMaxIt; ++it) {
-    int u = it * kWave + lane;
-    bool ok = u < n_items;
-    int ocl = ok ? u / a.NC2 : 0;
-    int r = ok ? u - ocl * a.NC2 : 0;
-    int dy = r / a.NC, dx = r - dy * a.NC;
-    it_ok[it] = ok;
-    it_oc[it] = ocl;
-    it_r[it] = r;
-    it_qoff[it] = ocl * a.IC * KK - dy * a.S * a.K - dx * a.S;
-    int vt = qz.vth_scalar;
-    if (qz.vth_kind == SALT_VTH_PER_CHANNEL) vt = qz.vth[oc0 + ocl];
-    it_vth[it] = vt;
-  }
-  const int pdy = lane / a.NC, pdx = lane - (lane / a.NC) * a.NC;
+  for (int it = 0; it < NIT; ++it) uf[it] = (float)(it * kWave + lane) + 0.5f;
 
   int vmin_l = 0, vmax_l = 0;
   int out_base = 0;
@@ -258,13 +289,13 @@ __global__ void __launch_bounds__(64) conv_layer_kernel(ConvArgs a) {
     // Decode 64 events at once, one per lane (connectivity/conv.py:15-43).
     const int j = base + lane;
     const bool ok = j < n_eff;
-    float tv = ok ? tb[j] : 0.0f;
-    int sv = ok ? sb[j] : -1;
+    const float tv = ok ? tb[j] : 0.0f;
+    const int sv = ok ? sb[j] : -1;
     bool rel = ok && sv >= 0;
     int c = 0, y = 0, x = 0;
     if (rel) {
       c = sv / a.HWin;
-      int rem = sv - c * a.HWin;
+      const int rem = sv - c * a.HWin;
       y = rem / a.Win;
       x = rem - y * a.Win;
       c = min(c, a.IC - 1);  // memory safety only; the host rejects such ids
@@ -272,84 +303,117 @@ __global__ void __launch_bounds__(64) conv_layer_kernel(ConvArgs a) {
     const int oy0 = floordiv_pos(y + a.P - a.K + a.S, a.S);  // ceil((y+P-K+1)/S)
     const int ox0 = floordiv_pos(x + a.P - a.K + a.S, a.S);
     const int oyA = max(oy0, r0), oyB = min((y + a.P) / a.S, r0 + rn - 1);
-    const int oxA = max(ox0, 0), oxB = min((x + a.P) / a.S, a.W - 1);
+    const int oxA = max(ox0, 0), oxB = min((x + a.P) / a.S, W - 1);
     rel = rel && oyA <= oyB && oxA <= oxB;
-    const int qe = c * KK + (y + a.P - oy0 * a.S) * a.K + (x + a.P - ox0 * a.S);
+    // Packed per-event fields: rectangle origin and size in candidate units, the
+    // partition position of its first cell, and the weight-code offset of that cell.
+    const int dyA = oyA - oy0, dxA = oxA - ox0;
+    const int rect = dyA | (dxA << 8) | ((oyB - oyA + 1) << 16) | ((oxB - oxA + 1) << 24);
+    const int pbase = (oyA - r0) * W + oxA;
+    const int qe4 = (c * KK + (y + a.P - oyA * a.S) * a.K + (x + a.P - oxA * a.S)) * 4;
     uint64_t todo = __ballot(rel);
 
     while (todo) {
       const int e = __builtin_ctzll(todo);
       todo &= todo - 1;
       const float te = rdlanef(tv, e);
-      const int oy0e = rdlane(oy0, e), ox0e = rdlane(ox0, e);
-      const int oyAe = rdlane(oyA, e), oyBe = rdlane(oyB, e);
-      const int oxAe = rdlane(oxA, e), oxBe = rdlane(oxB, e);
-      const int qee = rdlane(qe, e);
-      const int je = base + e;
+      const int rect_e = rdlane(rect, e);
+      const int pbase_e = rdlane(pbase, e);
+      const int qe4_e = rdlane(qe4, e);
+      const int ny = (rect_e >> 16) & 0xFF, nx = (int)((uint32_t)rect_e >> 24);
+      const int area = ny * nx;
+      const int items = ocn * area;
+      const int nit_e = (items + kWave - 1) >> 6;
+      const float inv_area = __builtin_amdgcn_rcpf((float)area);
+      const float inv_nx = __builtin_amdgcn_rcpf((float)nx);
 
-      // Position phase: lane r = dy*NC + dx resolves candidate (oy0+dy, ox0+dx).
-      const int oy = oy0e + pdy, ox = ox0e + pdx;
-      const bool pv = lane < a.NC2 && oy >= oyAe && oy <= oyBe && ox >= oxAe && ox <= oxBe;
-      int pack = -1, lpos = 0, cb = 0;
-      bool act = false;
-      if (pv) {
-        lpos = (oy - r0) * a.W + ox;
-        cb = cnt[lpos];
-        act = cb < a.mql;  // queue full: the event is dropped (connectivity/conv.py:143-151)
-        const int A = ext[decay_index(te - tl[lpos], qz.n_table)];
-        if (act) pack = (lpos << 16) | (A & 0xFFFF);
-      }
-
-      // Update phase: one (channel, position) register per lane.
+      // Round trip 1: register, code, threshold, last-update time, queue count.
+      int v[NIT], qv[NIT], vt[NIT], cb[NIT], lp[NIT], nl4[NIT], ocv[NIT], pv[NIT];
+      int mnv[NIT], mxv[NIT];
+      float tlv[NIT];
+      bool val[NIT];
 #pragma unroll
-      for (int it = 0; it < kMaxIt; ++it) {
-        if (it >= nit) break;
-        const int pk = __shfl(pack, it_r[it]);
-        const bool av = it_ok[it] && pk != -1;
-        bool fire = false;
-        int neuron = 0;
-        if (av) {
-          const int lp = pk >> 16;
-          const int A = pk & 0xFFFF;
-          const int nl = it_oc[it] * PW + lp;
-          const int32_t v = Vs[nl];
-          const int32_t qv = qs[it_qoff[it] + qee];
-          neuron = (oc0 + it_oc[it]) * a.HW + r0 * a.W + lp;
-          int vt = it_vth[it];
-          if (qz.vth_kind == SALT_VTH_PER_NEURON) vt = qz.vth[neuron];
-          const int32_t d = decay_mul<FAST24>(v, A, qz.fa, qz.rc);
-          const int32_t u = (int32_t)((uint32_t)d + ((uint32_t)qv << qz.fV));
-          const int32_t f = fit_bits(u, qz);
-          fire = has_vth && f >= vt;
-          Vs[nl] = fire ? 0 : f;
-          vmin_l = min(vmin_l, u);
-          vmax_l = max(vmax_l, u);
+      for (int it = 0; it < NIT; ++it) {
+        if (it < nit_e) {
+          // All index products are small: 24-bit multiplies (full rate).
+          const int u = it * kWave + lane;
+          val[it] = u < items;
+          const int oc = min((int)(uf[it] * inv_area), ocn - 1);
+          const int p = u - __mul24(oc, area);
+          const int dy = (int)(((float)p + 0.5f) * inv_nx);
+          const int dx = p - __mul24(dy, nx);
+          const int lp_raw = pbase_e + __mul24(dy, W) + dx;
+          const int q4_raw = __mul24(oc, ICKK4) - __mul24(dy, SK4) - __mul24(dx, S4) + qe4_e;
+          lp[it] = val[it] ? lp_raw : 0;  // lanes without an item read in-range words
+          ocv[it] = oc;
+          pv[it] = p;
+          nl4[it] = __mul24(oc, PW4) + lp[it] * 4;
+          const int q4 = val[it] ? q4_raw : 0;
+          const int vaddr = val[it] ? vs4 + nl4[it] : trash4;
+          v[it] = lds_at<int32_t>(lds, vaddr);
+          qv[it] = lds_at<int32_t>(lds, qs4 + q4);
+          vt[it] = VTHN ? lds_at<int32_t>(lds, val[it] ? th4 + nl4[it] : trash4)
+                        : lds_at<int32_t>(lds, vthc4 + (val[it] ? oc : 0) * 4);
+          tlv[it] = lds_at<float>(lds, tl4 + lp[it] * 4);
+          cb[it] = lds_at<int32_t>(lds, cnt4 + lp[it] * 4);
           if (EXT) {
-            mn[nl] = min(mn[nl], u);
-            mx[nl] = max(mx[nl], u);
+            mnv[it] = lds_at<int32_t>(lds, val[it] ? mn4 + nl4[it] : trash4);
+            mxv[it] = lds_at<int32_t>(lds, val[it] ? mx4 + nl4[it] : trash4);
           }
         }
-        if (a.direct) {
+      }
+      // Round trip 2: decay codes (salt_core/quant/codes.py:87-105; index 0 = identity).
+      int A[NIT];
+#pragma unroll
+      for (int it = 0; it < NIT; ++it)
+        if (it < nit_e)
+          A[it] = lds_at<int32_t>(lds, ext4 + 4 * (int)fminf(fmaxf(te - tlv[it], 0.0f), tab_top));
+      // Update (salt_core/quant/scan.py:22-52), write back, emit spikes.
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        if (it < nit_e) {
+          const bool act = val[it] && cb[it] < a.mql;  // a full queue drops the event
+          const int32_t d = decay_mul<FAST24>(v[it], A[it], qz.fa, qz.rc);
+          const int32_t u = (int32_t)((uint32_t)d + ((uint32_t)qv[it] << qfV));
+          const int32_t f = fit_bits(u, qz);
+          const bool fire = act && has_vth && f >= vt[it];
+          lds_put<int32_t>(lds, act ? vs4 + nl4[it] : trash4, fire ? 0 : f);
+          const int um = act ? u : 0;
+          vmin_l = min(vmin_l, um);
+          vmax_l = max(vmax_l, um);
+          if (EXT) {
+            lds_put<int32_t>(lds, act ? mn4 + nl4[it] : trash4, min(mnv[it], u));
+            lds_put<int32_t>(lds, act ? mx4 + nl4[it] : trash4, max(mxv[it], u));
+          }
           const uint64_t bal = __ballot(fire);
-          if (fire) {
-            const int idx = out_base + __popcll(bal & lanemask_lt(lane));
-            if (idx < a.cap) {
-              a.out_t[(size_t)b * a.cap + idx] = te;
-              a.out_s[(size_t)b * a.cap + idx] = neuron;
+          if (bal) {
+            const int neuron = (oc0 + ocv[it]) * a.HW + r0 * W + lp[it];
+            if (a.direct) {
+              if (fire) {
+                const int idx = out_base + __popcll(bal & lanemask_lt(lane));
+                if (idx < a.cap) {
+                  a.out_t[(size_t)b * a.cap + idx] = te;
+                  a.out_s[(size_t)b * a.cap + idx] = neuron;
+                }
+              }
+              out_base += __popcll(bal);
+            } else if (fire) {
+              // Candidate index within the event's NC x NC grid = mask bit.
+              const int dy = pv[it] / nx, dx = pv[it] - (pv[it] / nx) * nx;
+              const int r = ((rect_e & 0xFF) + dy) * a.NC + (((rect_e >> 8) & 0xFF) + dx);
+              const size_t w = ((size_t)b * L + base + e) * (size_t)(a.OC * a.WPO) +
+                               (size_t)(oc0 + ocv[it]) * a.WPO + (r >> 5);
+              atomicOr(&a.masks[w], 1u << (r & 31));
             }
           }
-          out_base += __popcll(bal);
-        } else if (fire) {
-          const size_t w = ((size_t)b * L + je) * (size_t)(a.OC * a.WPO) +
-                           (size_t)(oc0 + it_oc[it]) * a.WPO + (it_r[it] >> 5);
-          atomicOr(&a.masks[w], 1u << (it_r[it] & 31));
         }
       }
-
-      // Commit phase: queue counter and last-update time of the touched positions.
-      if (pv) {
-        cnt[lpos] = cb + 1;
-        if (act) tl[lpos] = te;
+      // Commit the touched positions' queue count and last-update time (channel-0
+      // items, which are the first `area` lanes of iteration 0).
+      {
+        const bool commit = lane < area;
+        lds_put<int32_t>(lds, commit ? cnt4 + lp[0] * 4 : trash4, cb[0] + 1);
+        lds_put<float>(lds, (commit && cb[0] < a.mql) ? tl4 + lp[0] * 4 : trash4, te);
       }
       asm volatile("" ::: "memory");  // keep this event's LDS traffic before the next one's
     }
@@ -362,22 +426,22 @@ __global__ void __launch_bounds__(64) conv_layer_kernel(ConvArgs a) {
   for (int i = lane; i < PW; i += kWave) maxcnt = max(maxcnt, cnt[i]);
   for (int li = lane; li < ocn * PW; li += kWave) {
     const int ocl = li / PW;
-    const int lp = li - ocl * PW;
-    const int cb = cnt[lp];
-    int32_t v = Vs[li];
-    if (cb < a.mql) {
-      const float dt = cb > 0 ? T - tl[lp] : 0.0f;
-      const int A = ext[decay_index(dt, qz.n_table)];
-      v = decay_mul<FAST24>(v, A, qz.fa, qz.rc);  // |D| <= |V|: in range, cannot fire
-      vmin_l = min(vmin_l, v);
-      vmax_l = max(vmax_l, v);
+    const int lpp = li - ocl * PW;
+    const int cbv = cnt[lpp];
+    int32_t vv = Vs[li];
+    if (cbv < a.mql) {
+      const float dt = cbv > 0 ? T - tl[lpp] : 0.0f;
+      const int A = ext[(int)fminf(fmaxf(dt, 0.0f), tab_top)];
+      vv = decay_mul<FAST24>(vv, A, qz.fa, qz.rc);  // |D| <= |V|: in range, cannot fire
+      vmin_l = min(vmin_l, vv);
+      vmax_l = max(vmax_l, vv);
       if (EXT) {
-        mn[li] = min(mn[li], v);
-        mx[li] = max(mx[li], v);
+        mn[li] = min(mn[li], vv);
+        mx[li] = max(mx[li], vv);
       }
     }
-    const size_t ng = (size_t)b * (a.OC * a.HW) + (size_t)(oc0 + ocl) * a.HW + r0 * a.W + lp;
-    if (a.v_final) a.v_final[ng] = v;
+    const size_t ng = (size_t)b * (a.OC * a.HW) + (size_t)(oc0 + ocl) * a.HW + r0 * W + lpp;
+    if (a.v_final) a.v_final[ng] = vv;
     if (EXT) {
       a.v_min[ng] = mn[li];
       a.v_max[ng] = mx[li];
@@ -415,6 +479,7 @@ struct FcArgs {
   Quant qz;
   const int32_t* table;
   const void* qt;          // (n_in, n_out)
+  int q_bits;
   int L;
   const float* times;
   const int32_t* src;
@@ -431,16 +496,26 @@ struct FcArgs {
 };
 
 // One wave = one stream x one slice of 64*NPL neurons, neuron = n0 + k*64 + lane.
-// connectivity/fc.py:20-33, 54-61; layers/fc.py:84-124.
-template <typename QT, int NPL, bool FAST24>
+// connectivity/fc.py:20-33, 54-61; layers/fc.py:84-124.  WLDS: the slice's weight
+// columns (n_in x slice, native width) are staged in LDS; otherwise they are read from the
+// transposed global copy, one event ahead.
+template <typename QT, int NPL, bool FAST24, bool WLDS>
 __global__ void __launch_bounds__(64) fc_layer_kernel(FcArgs a) {
   extern __shared__ int32_t dyn[];
   const int lane = threadIdx.x;
   const int b = blockIdx.y;
   const int n0 = blockIdx.x * (kWave * NPL);
+  const int sw = min(kWave * NPL, a.n_out - n0);  // neurons in this slice
   const Quant& qz = a.qz;
   int32_t* tab = dyn;
+  QT* wl = reinterpret_cast<QT*>(dyn + (qz.n_table + 2));
+  const QT* qt = static_cast<const QT*>(a.qt);
   load_ext_table(tab, a.table, qz.n_table, qz.fa, lane);
+  if (WLDS)
+    for (int i = lane; i < a.n_in * sw; i += kWave) {
+      const int r = i / sw;
+      wl[i] = qt[(size_t)r * a.n_out + n0 + (i - r * sw)];
+    }
   __syncthreads();
 
   int32_t V[NPL], mn[NPL], mx[NPL], vth[NPL];
@@ -456,12 +531,12 @@ __global__ void __launch_bounds__(64) fc_layer_kernel(FcArgs a) {
              : (qz.vth_kind != SALT_VTH_NONE && nv[k]) ? qz.vth[n] : 0;
   }
   const bool has_vth = qz.vth_kind != SALT_VTH_NONE;
+  const float tab_top = (float)(qz.n_table + 1);
   const int L = a.L;
   const int nr = a.n_real[b];
   const int n_eff = nr < 0 ? 0 : (nr < L ? nr : L);
   const float* tb = a.times + (size_t)b * L;
   const int32_t* sb = a.src + (size_t)b * L;
-  const QT* qt = static_cast<const QT*>(a.qt);
   float t_prev = 0.0f;  // the first event is compared with t = 0 (fc.py:30)
   int out_base = 0;
 
@@ -471,26 +546,31 @@ __global__ void __launch_bounds__(64) fc_layer_kernel(FcArgs a) {
     const float tv = ok ? tb[j] : 0.0f;
     const int sv = ok ? min(max(sb[j], 0), a.n_in - 1) : 0;
     const int ne = min(kWave, n_eff - base);
-    // Prefetch the weight column of the first event of the chunk.
     int32_t qn[NPL];
-    {
+    if (!WLDS) {
       const int s0 = rdlane(sv, 0);
 #pragma unroll
       for (int k = 0; k < NPL; ++k)
         qn[k] = nv[k] ? (int32_t)qt[(size_t)s0 * a.n_out + n0 + k * kWave + lane] : 0;
     }
     for (int e = 0; e < ne; ++e) {
+      const int se = rdlane(sv, e);
       int32_t qc[NPL];
+      if (WLDS) {
 #pragma unroll
-      for (int k = 0; k < NPL; ++k) qc[k] = qn[k];
-      if (e + 1 < ne) {
-        const int s1 = rdlane(sv, e + 1);
+        for (int k = 0; k < NPL; ++k) qc[k] = nv[k] ? (int32_t)wl[se * sw + k * kWave + lane] : 0;
+      } else {
 #pragma unroll
-        for (int k = 0; k < NPL; ++k)
-          qn[k] = nv[k] ? (int32_t)qt[(size_t)s1 * a.n_out + n0 + k * kWave + lane] : 0;
+        for (int k = 0; k < NPL; ++k) qc[k] = qn[k];
+        if (e + 1 < ne) {
+          const int s1 = rdlane(sv, e + 1);
+#pragma unroll
+          for (int k = 0; k < NPL; ++k)
+            qn[k] = nv[k] ? (int32_t)qt[(size_t)s1 * a.n_out + n0 + k * kWave + lane] : 0;
+        }
       }
       const float te = rdlanef(tv, e);
-      const int A = tab[decay_index(te - t_prev, qz.n_table)];
+      const int A = tab[(int)fminf(fmaxf(te - t_prev, 0.0f), tab_top)];
       t_prev = te;
 #pragma unroll
       for (int k = 0; k < NPL; ++k) {
@@ -506,14 +586,16 @@ __global__ void __launch_bounds__(64) fc_layer_kernel(FcArgs a) {
         }
         const uint64_t bal = __ballot(fire);
         if (a.direct) {
-          if (fire) {
-            const int idx = out_base + __popcll(bal & lanemask_lt(lane));
-            if (idx < a.cap) {
-              a.out_t[(size_t)b * a.cap + idx] = te;
-              a.out_s[(size_t)b * a.cap + idx] = n0 + k * kWave + lane;
+          if (bal) {
+            if (fire) {
+              const int idx = out_base + __popcll(bal & lanemask_lt(lane));
+              if (idx < a.cap) {
+                a.out_t[(size_t)b * a.cap + idx] = te;
+                a.out_s[(size_t)b * a.cap + idx] = n0 + k * kWave + lane;
+              }
             }
+            out_base += __popcll(bal);
           }
-          out_base += __popcll(bal);
         } else {
           const int w0 = (n0 + k * kWave) >> 5;
           if (lane < 2 && w0 + lane < a.words)
@@ -698,14 +780,14 @@ struct ConvPlan {
   size_t lds;
 };
 
-size_t conv_lds_bytes(const salt_layer_desc* d, int n_table, int G, int R, int W, bool ext) {
-  size_t words = (size_t)(n_table + 2) + (size_t)G * d->ic * d->k * d->k +
-                 (size_t)G * R * W * (ext ? 3 : 1) + 2 * (size_t)R * W;
-  return words * 4;
+size_t conv_lds_bytes(const salt_layer_desc* d, int n_table, int G, int R, int W, bool ext,
+                      bool vthn) {
+  return conv_lds_words(n_table, G, d->ic, d->k, R, W, ext, vthn) * 4;
 }
 
 int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext,
                   ConvPlan* pl) {
+  const bool vthn = p->v_th_kind == SALT_VTH_PER_NEURON;
   pl->H = (d->h_in + 2 * d->p - d->k) / d->s + 1;
   pl->W = (d->w_in + 2 * d->p - d->k) / d->s + 1;
   if (pl->H < 1 || pl->W < 1) return fail(-1, "conv geometry gives an empty output plane");
@@ -720,7 +802,7 @@ int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool e
   const int gmax_it = std::max(1, (kMaxIt * kWave) / pl->NC2);
   // Whole layer in one wave per stream when it fits and the batch alone fills the GPU.
   if (OC <= gmax_it && pl->HW <= kMaxPartPositions) {
-    size_t lds = conv_lds_bytes(d, p->n_table, OC, H, W, ext);
+    size_t lds = conv_lds_bytes(d, p->n_table, OC, H, W, ext, vthn);
     if ((lds <= 40 * 1024 && B >= 512) || (lds <= (size_t)kLdsMax && B >= 2048)) {
       pl->G = OC; pl->R = H; pl->n_og = 1; pl->n_rb = 1; pl->direct = 1; pl->lds = lds;
       return 0;
@@ -731,10 +813,10 @@ int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool e
   int G = std::max(1, std::min(OC, (2 * kWave) / pl->NC2));
   for (;;) {
     int R = H;
-    while (R > 1 && (conv_lds_bytes(d, p->n_table, G, R, W, ext) > (size_t)kLdsPartBudget ||
+    while (R > 1 && (conv_lds_bytes(d, p->n_table, G, R, W, ext, vthn) > (size_t)kLdsPartBudget ||
                      (size_t)R * W > (size_t)kMaxPartPositions))
       --R;
-    if (conv_lds_bytes(d, p->n_table, G, R, W, ext) > (size_t)kLdsMax ||
+    if (conv_lds_bytes(d, p->n_table, G, R, W, ext, vthn) > (size_t)kLdsMax ||
         (size_t)R * W > (size_t)kMaxPartPositions) {
       if (G == 1) return fail(-3, "conv: one output row does not fit in LDS (w_out=%d)", W);
       G = (G + 1) / 2;
@@ -747,7 +829,7 @@ int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool e
     }
     pl->G = G; pl->R = R; pl->n_og = n_og; pl->n_rb = n_rb;
     pl->direct = (n_og == 1 && n_rb == 1);
-    pl->lds = conv_lds_bytes(d, p->n_table, G, R, W, ext);
+    pl->lds = conv_lds_bytes(d, p->n_table, G, R, W, ext, vthn);
     return 0;
   }
 }
@@ -835,9 +917,9 @@ int32_t fill(int32_t* p, int32_t v, size_t n, hipStream_t st) {
   return 0;
 }
 
-template <typename QT, bool F24, bool EXT>
+template <bool F24, bool EXT, bool VTHN, int NIT>
 int32_t launch_conv_t(const ConvArgs& a, const ConvPlan& pl, int B, hipStream_t st) {
-  auto kern = conv_layer_kernel<QT, F24, EXT>;
+  auto kern = conv_layer_kernel<F24, EXT, VTHN, NIT>;
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
     HIP_TRY(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -849,20 +931,37 @@ int32_t launch_conv_t(const ConvArgs& a, const ConvPlan& pl, int B, hipStream_t 
   return 0;
 }
 
-template <typename QT>
-int32_t launch_conv_q(const ConvArgs& a, const ConvPlan& pl, int B, bool f24, bool ext,
-                      hipStream_t st) {
-  if (f24) return ext ? launch_conv_t<QT, true, true>(a, pl, B, st)
-                      : launch_conv_t<QT, true, false>(a, pl, B, st);
-  return ext ? launch_conv_t<QT, false, true>(a, pl, B, st)
-             : launch_conv_t<QT, false, false>(a, pl, B, st);
+template <bool F24, bool EXT, bool VTHN>
+int32_t launch_conv_n(const ConvArgs& a, const ConvPlan& pl, int B, hipStream_t st) {
+  const int nit = (pl.G * pl.NC2 + kWave - 1) / kWave;
+  if (nit <= 1) return launch_conv_t<F24, EXT, VTHN, 1>(a, pl, B, st);
+  if (nit <= 2) return launch_conv_t<F24, EXT, VTHN, 2>(a, pl, B, st);
+  if (nit <= 4) return launch_conv_t<F24, EXT, VTHN, 4>(a, pl, B, st);
+  return launch_conv_t<F24, EXT, VTHN, kMaxIt>(a, pl, B, st);
 }
 
-template <typename QT, int NPL, bool F24>
+int32_t launch_conv(const ConvArgs& a, const ConvPlan& pl, int B, bool f24, bool ext, bool vthn,
+                    hipStream_t st) {
+  if (f24) {
+    if (ext) return vthn ? launch_conv_n<true, true, true>(a, pl, B, st)
+                         : launch_conv_n<true, true, false>(a, pl, B, st);
+    return vthn ? launch_conv_n<true, false, true>(a, pl, B, st)
+                : launch_conv_n<true, false, false>(a, pl, B, st);
+  }
+  if (ext) return vthn ? launch_conv_n<false, true, true>(a, pl, B, st)
+                       : launch_conv_n<false, true, false>(a, pl, B, st);
+  return vthn ? launch_conv_n<false, false, true>(a, pl, B, st)
+              : launch_conv_n<false, false, false>(a, pl, B, st);
+}
+
+constexpr size_t kFcWeightLds = 40 * 1024;  // stage FC weight slices up to this size
+
+template <typename QT, int NPL, bool F24, bool WLDS>
 int32_t launch_fc_t(const FcArgs& a, const FcPlan& pl, int B, hipStream_t st) {
-  size_t lds = (size_t)(a.qz.n_table + 2) * 4;
+  const int sw = std::min(kWave * NPL, a.n_out);
+  size_t lds = (size_t)(a.qz.n_table + 2) * 4 + (WLDS ? (size_t)a.n_in * sw * sizeof(QT) : 0);
   if (lds > (size_t)kLdsMax) return fail(-3, "decay table too long for LDS");
-  auto kern = fc_layer_kernel<QT, NPL, F24>;
+  auto kern = fc_layer_kernel<QT, NPL, F24, WLDS>;
   static bool attr_set = false;
   if (!attr_set) {
     HIP_TRY(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -874,14 +973,22 @@ int32_t launch_fc_t(const FcArgs& a, const FcPlan& pl, int B, hipStream_t st) {
   return 0;
 }
 
+template <typename QT, int NPL, bool F24>
+int32_t launch_fc_w(const FcArgs& a, const FcPlan& pl, int B, hipStream_t st) {
+  const size_t wbytes = (size_t)a.n_in * std::min(kWave * NPL, a.n_out) * sizeof(QT);
+  if (wbytes + (size_t)(a.qz.n_table + 2) * 4 <= kFcWeightLds)
+    return launch_fc_t<QT, NPL, F24, true>(a, pl, B, st);
+  return launch_fc_t<QT, NPL, F24, false>(a, pl, B, st);
+}
+
 template <typename QT, bool F24>
 int32_t launch_fc_npl(const FcArgs& a, const FcPlan& pl, int B, hipStream_t st) {
   switch (pl.npl) {
-    case 1: return launch_fc_t<QT, 1, F24>(a, pl, B, st);
-    case 2: return launch_fc_t<QT, 2, F24>(a, pl, B, st);
-    case 4: return launch_fc_t<QT, 4, F24>(a, pl, B, st);
-    case 8: return launch_fc_t<QT, 8, F24>(a, pl, B, st);
-    default: return launch_fc_t<QT, 16, F24>(a, pl, B, st);
+    case 1: return launch_fc_w<QT, 1, F24>(a, pl, B, st);
+    case 2: return launch_fc_w<QT, 2, F24>(a, pl, B, st);
+    case 4: return launch_fc_w<QT, 4, F24>(a, pl, B, st);
+    case 8: return launch_fc_w<QT, 8, F24>(a, pl, B, st);
+    default: return launch_fc_w<QT, 16, F24>(a, pl, B, st);
   }
 }
 
@@ -1007,7 +1114,7 @@ int32_t salt_layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     a.H = pl.H; a.W = pl.W; a.HW = pl.HW; a.NC = pl.NC; a.NC2 = pl.NC2; a.WPO = pl.WPO;
     a.mql = desc->max_queue_len;
     a.G = pl.G; a.n_og = pl.n_og; a.R = pl.R;
-    a.qz = qz; a.table = prm->d_decay_table; a.q = prm->d_q;
+    a.qz = qz; a.table = prm->d_decay_table; a.q = prm->d_q; a.q_bits = prm->q_bits;
     a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
     a.cap = out->cap; a.fill_pads = out->fill_pads; a.direct = pl.direct;
     a.out_t = out->d_times; a.out_s = out->d_src; a.out_n = out->d_n;
@@ -1018,11 +1125,7 @@ int32_t salt_layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
       if ((rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
       if ((rc = fill(reinterpret_cast<int32_t*>(a.masks), 0, need / 4, st))) return rc;
     }
-    switch (prm->q_bits) {
-      case 8: rc = launch_conv_q<int8_t>(a, pl, B, f24, ext, st); break;
-      case 16: rc = launch_conv_q<int16_t>(a, pl, B, f24, ext, st); break;
-      default: rc = launch_conv_q<int32_t>(a, pl, B, f24, ext, st); break;
-    }
+    rc = launch_conv(a, pl, B, f24, ext, prm->v_th_kind == SALT_VTH_PER_NEURON, st);
     if (rc) return rc;
     if (!pl.direct) {
       CompactArgs c;
@@ -1045,7 +1148,7 @@ int32_t salt_layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     return fail(-1, "workspace of %zu bytes below the %zu needed", workspace_bytes, need);
   FcArgs a;
   a.n_in = desc->n_in; a.n_out = desc->n_out; a.words = pl.words;
-  a.qz = qz; a.table = prm->d_decay_table; a.qt = prm->d_q;
+  a.qz = qz; a.table = prm->d_decay_table; a.qt = prm->d_q; a.q_bits = prm->q_bits;
   a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
   a.cap = out->cap; a.fill_pads = out->fill_pads; a.direct = pl.direct;
   a.out_t = out->d_times; a.out_s = out->d_src; a.out_n = out->d_n;
