@@ -1,0 +1,475 @@
+// Event-driven integer conv layer (salt_core/layers/conv.py:124-149 with the queue of
+// salt_core/connectivity/conv.py and the scan of salt_core/quant/scan.py:22-132).
+//
+// A work-group owns one (stream, band of R output rows); its nw wavefronts split the
+// output channels (channel group = wave), and every wave consumes all of the stream's
+// events in order.  Everything a wave touches per event lives in LDS: registers
+// V[channel slot][position], per-position (last-update time, queue count), its weight
+// codes, and the shared extended decay table.
+//
+// Lane mapping.  NC = (k-1)//s + 1 candidate rows (and columns) per input event and
+// NC2 = NC*NC candidates; lane l is channel slot l / NC2 (+ Gi per iteration) and
+// candidate (dy, dx) = divmod(l % NC2, NC).  Relative to an event's first candidate
+// (oy0, ox0) = (ceil((y+P-K+1)/S), ceil((x+P-K+1)/S)) every address a lane needs is an
+// event-uniform base plus a lane constant:
+//   V slot    = ((oy0-r0)*W + ox0) + [slot*VS + dy*W + dx]
+//   weight    = (c*K*K + (y+P-oy0*S)*K + (x+P-ox0*S)) + [slot*QS - dy*S*K - dx*S]
+// (VS, QS: the odd per-slot strides of the register and weight arrays), so the
+// per-event loop does no index arithmetic beyond adds.  Each wave decodes 64 events at
+// a time (one per lane) into LDS records: those two bases, the time and a 64-bit mask
+// of the candidates inside the output plane and the band; the loop reads one record
+// per event (a broadcast LDS read).
+//
+// Channel slots past a wave's channels hold zero weights and an unreachable
+// threshold: their registers stay 0, never fire and never move the extremes (which
+// start at 0), so no lane needs a per-iteration predicate.
+//
+// Output.  When the work-group holds the whole output plane (one band), each wave
+// stores the ballot of its spikes per (event, iteration) in LDS, and after every
+// 64-event chunk wave 0 walks them in (event, wave, iteration, lane) order -- which is
+// (event, ascending neuron id), the order of salt_core/stream.py:24-46 -- and appends
+// the spikes to the stream.  With several bands each wave sets per-event spike bits
+// in global memory instead, and a compaction kernel orders them.
+//
+// No barrier inside the event loop: a wave's LDS operations complete in program
+// order, so event e+1 reads what event e wrote.
+#pragma once
+
+#include "salt_device.hpp"
+
+namespace salt {
+
+constexpr int kConvMaxWaves = 8;  // channel groups (waves) per work-group
+
+struct ConvArgs {
+  // geometry
+  int IC, Win, HWin, OC, K, S, P, H, W, HW, NC, NC2, WPO, mql;
+  // partition: G channels per wave in NIT iterations of Gi slots, nw waves (channel
+  // groups) per work-group, R output rows per band
+  int G, Gi, nw, R;
+  // quantisation
+  Quant qz;
+  const int32_t* table;
+  const void* q;
+  int q_bits;
+  // events
+  int L;
+  const float* times;
+  const int32_t* src;
+  const int32_t* n_real;
+  // outputs
+  int cap, fill_pads, merge;  // merge: one band, ordered output written in-kernel
+  float* out_t;
+  int32_t* out_s;
+  int32_t* out_n;
+  int32_t* v_final;
+  int32_t* v_min;
+  int32_t* v_max;
+  int32_t* stats;
+  uint32_t* masks;
+};
+
+// LDS layout of a work-group, in 4-byte words: a shared part (decay table, ballot-bit
+// map, reduction slots), then one region per wave.
+struct ConvLds {
+  int ext, lanemap, red, shared_words;                                // shared
+  int rec, rec1, stg, tc, vthc, qs, v, mn, mx, th, wave_words;        // per wave
+  int vs, qst;  // odd slot strides of the register and weight arrays
+  int words;
+};
+
+__host__ __device__ inline ConvLds conv_lds_layout(int n_table, int nw, int Gp, int nit,
+                                                   int ICKK, int PWs, bool ext, bool vthn) {
+  ConvLds l;
+  l.vs = PWs | 1;
+  l.qst = ICKK | 1;
+  int o = 0;
+  l.ext = o;     o += n_table + 2;
+  l.lanemap = o; o += 2 * kWave;               // int2 {slot, position offset} per lane
+  l.red = o;     o += 4 * kConvMaxWaves;
+  o = (o + 3) & ~3;
+  l.shared_words = o;
+  int w = 0;
+  l.rec = w;  w += kWave * 4;     // int4 {t, V base, weight base, candidate mask low}
+  l.rec1 = w; w += kWave * 2;     // int2 {candidate mask high, event index}
+  l.stg = w;  w += kWave * nit * 2;  // uint64 spike ballot per (event, iteration)
+  l.tc = w;   w += 2 * PWs;       // int2 {last-update time, queue count} per position
+  l.vthc = w; w += Gp;
+  l.qs = w;   w += Gp * l.qst;
+  l.v = w;    w += Gp * l.vs;
+  l.mn = w;   w += ext ? Gp * l.vs : 0;
+  l.mx = w;   w += ext ? Gp * l.vs : 0;
+  l.th = w;   w += vthn ? Gp * l.vs : 0;
+  w = (w + 3) & ~3;
+  l.wave_words = w;
+  l.words = l.shared_words + nw * w;
+  return l;
+}
+
+// Per-lane constants and LDS pointers of one wave (see the file comment).
+struct ConvLane {
+  int4* rec;
+  int2* rec1;
+  uint64_t* stg;
+  int2* tc;
+  int32_t* ext;
+  int32_t* qs;
+  int32_t* Vs;
+  int32_t* mn;
+  int32_t* mx;
+  int32_t* th;
+  uint64_t lm;      // this lane's candidate bit (0 for lanes without a slot)
+  int first;        // slot 0: the lane that commits its position's time and count
+  int lp, lv, lq;   // position / register / weight offsets relative to an event's bases
+  int GiVS, GiQS;
+  int cand, oc_lane, r0, W, HW, mql, ntab;
+};
+
+// The events of one decoded chunk, in order (salt_core/quant/scan.py:22-52 per update).
+// MERGE: stage the spike ballots for the work-group's merge; otherwise set the
+// partition's spike bits in global memory.
+template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, bool MERGE>
+__device__ __forceinline__ void conv_events(const ConvArgs& a, const ConvLane& c,
+                                            const int (&vtc)[NIT], int n_ev, int b,
+                                            int& vmin_l, int& vmax_l) {
+  if (n_ev == 0) return;
+  const Quant& qz = a.qz;
+  const int fa = qz.fa, rc = qz.rc;
+  const int lane = threadIdx.x & (kWave - 1);
+  // Software pipeline: the record of event e+1 and its positions' (time, count) are
+  // read while event e is processed (after e's own count/time write, so they are
+  // current), which leaves one LDS round trip per event: decay code, registers, codes.
+  int4 r = c.rec[0];
+  int2 r1 = c.rec1[0];
+  bool vc = ((((uint64_t)(uint32_t)r1.x << 32) | (uint32_t)r.w) & c.lm) != 0;
+  int pa = r.y + c.lp;
+  int2 st = make_int2(0, 0);
+  if (vc) st = c.tc[pa];
+  for (int e = 0; e < n_ev; ++e) {
+    const bool more = e + 1 < n_ev;
+    const int4 rn = c.rec[more ? e + 1 : e];
+    const int2 rn1 = c.rec1[more ? e + 1 : e];
+    int fire[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) fire[it] = 0;
+    // A position whose queue is full (max_queue_len real columns) drops the event and
+    // its time (connectivity/conv.py:57-99 truncates the queue).
+    const bool act = vc && st.y < c.mql;
+    int A = 0;
+    int v[NIT], qv[NIT], vt[NIT], mnv[NIT], mxv[NIT];
+    const int va = r.y + c.lv, qa = r.z + c.lq;
+    if (vc) {
+      if (c.first) c.tc[pa] = make_int2(act ? r.x : st.x, st.y + 1);
+      if (act) {
+        A = c.ext[decay_slot(r.x - st.x, c.ntab)];
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          v[it] = c.Vs[va + it * c.GiVS];
+          qv[it] = c.qs[qa + it * c.GiQS];
+          vt[it] = VTHN ? c.th[va + it * c.GiVS] : vtc[it];
+          if (EXT) { mnv[it] = c.mn[va + it * c.GiVS]; mxv[it] = c.mx[va + it * c.GiVS]; }
+        }
+      }
+    }
+    const bool vcn = more && ((((uint64_t)(uint32_t)rn1.x << 32) | (uint32_t)rn.w) & c.lm) != 0;
+    const int pan = rn.y + c.lp;
+    int2 stn = make_int2(0, 0);
+    if (vcn) stn = c.tc[pan];
+    if (act) {
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int32_t d = decay_mul<F24>(v[it], A, fa, rc);
+        const int32_t u = (int32_t)((uint32_t)d + (uint32_t)qv[it]);  // codes hold q*2^f_V
+        const int32_t f = fit_bits<SAT>(u, qz);
+        const bool fi = f >= vt[it];
+        fire[it] = fi ? 1 : 0;
+        c.Vs[va + it * c.GiVS] = fi ? 0 : f;
+        vmin_l = min(vmin_l, u);
+        vmax_l = max(vmax_l, u);
+        if (EXT) {
+          c.mn[va + it * c.GiVS] = min(mnv[it], u);
+          c.mx[va + it * c.GiVS] = max(mxv[it], u);
+        }
+      }
+    }
+    // Spikes, in uniform control flow.
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const uint64_t bal = __ballot(fire[it] != 0);
+      if (bal) {
+        if (MERGE) {
+          if (lane == 0) c.stg[e * NIT + it] = bal;
+        } else if (fire[it]) {
+          // Bit = candidate index in the event's NC x NC grid (compaction decodes it).
+          const size_t w = ((size_t)b * a.L + r1.y) * (size_t)(a.OC * a.WPO) +
+                           (size_t)(c.oc_lane + it * a.Gi) * a.WPO + (c.cand >> 5);
+          atomicOr(&a.masks[w], 1u << (c.cand & 31));
+        }
+      }
+    }
+    r = rn;
+    r1 = rn1;
+    vc = vcn;
+    pa = pan;
+    st = stn;
+    asm volatile("" ::: "memory");  // keep this event's LDS traffic before the next one's
+  }
+}
+
+template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN>
+__global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvArgs a) {
+  extern __shared__ int32_t smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);  // channel group
+  const int nthr = blockDim.x;
+  const int b = blockIdx.y;
+  const int rb = blockIdx.x;   // band
+  const int Gi = a.Gi, Gp = NIT * a.Gi;
+  const int oc0 = wv * a.G;
+  const int ocn = max(0, min(a.G, a.OC - oc0));
+  const int r0 = rb * a.R;
+  const int rn = min(a.R, a.H - r0);
+  const int W = a.W, PWs = a.R * W, PW = rn * W;
+  const int KK = a.K * a.K, ICKK = a.IC * KK;
+  const Quant& qz = a.qz;
+  const ConvLds lay = conv_lds_layout(qz.n_table, a.nw, Gp, NIT, ICKK, PWs, EXT, VTHN);
+  int32_t* wbase = smem + lay.shared_words + wv * lay.wave_words;
+  int2* lanemap = reinterpret_cast<int2*>(smem + lay.lanemap);
+  int32_t* red = smem + lay.red;
+  ConvLane c;
+  c.ext = smem + lay.ext;
+  c.rec = reinterpret_cast<int4*>(wbase + lay.rec);
+  c.rec1 = reinterpret_cast<int2*>(wbase + lay.rec1);
+  c.stg = reinterpret_cast<uint64_t*>(wbase + lay.stg);
+  c.tc = reinterpret_cast<int2*>(wbase + lay.tc);
+  int32_t* vthc = wbase + lay.vthc;
+  c.qs = wbase + lay.qs;
+  c.Vs = wbase + lay.v;
+  c.mn = wbase + lay.mn;
+  c.mx = wbase + lay.mx;
+  c.th = wbase + lay.th;
+  const int VS = lay.vs, QS = lay.qst;
+
+  // ---- shared state: decay table, ballot bit -> (slot, position offset)
+  load_ext_table(c.ext, a.table, qz.n_table, qz.fa, tid, nthr);
+  for (int k = tid; k < kWave; k += nthr) {
+    const int s = k / a.NC2, cd = k - s * a.NC2;
+    lanemap[k] = make_int2(s, (cd / a.NC) * W + (cd - (cd / a.NC) * a.NC));
+  }
+  // ---- this wave's state
+  for (int i = lane; i < Gp; i += kWave) {
+    int v = INT_MAX;  // unreachable: registers stay below 2^29
+    if (i < ocn) {
+      if (qz.vth_kind == SALT_VTH_SCALAR) v = qz.vth_scalar;
+      else if (qz.vth_kind == SALT_VTH_PER_CHANNEL) v = qz.vth[oc0 + i];
+    }
+    vthc[i] = v;
+  }
+  for (int i = lane; i < Gp * QS; i += kWave) {
+    const int s = i / QS, k = i - s * QS;
+    // Codes are stored pre-shifted: q * 2^f_V in two's complement, as U = D + q*2^f_V.
+    c.qs[i] = (s < ocn && k < ICKK)
+                  ? (int32_t)((uint32_t)load_code_bits(a.q, (size_t)(oc0 + s) * ICKK + k,
+                                                       a.q_bits) << qz.fV)
+                  : 0;
+  }
+  for (int i = lane; i < Gp * VS; i += kWave) {
+    c.Vs[i] = 0;
+    if (EXT) { c.mn[i] = 0; c.mx[i] = 0; }
+    if (VTHN) {
+      const int s = i / VS, p = i - s * VS;
+      c.th[i] = (s < ocn && p < PW) ? qz.vth[(size_t)(oc0 + s) * a.HW + r0 * W + p] : INT_MAX;
+    }
+  }
+  for (int i = lane; i < PWs; i += kWave) c.tc[i] = make_int2(0, 0);
+  __syncthreads();
+
+  // ---- lane constants
+  const int slot0 = lane / a.NC2;
+  c.cand = lane - slot0 * a.NC2;
+  const int dy = c.cand / a.NC, dx = c.cand - (c.cand / a.NC) * a.NC;
+  const bool lane_on = slot0 < Gi;
+  c.lm = lane_on ? (1ull << c.cand) : 0ull;
+  c.first = (lane_on && slot0 == 0) ? 1 : 0;
+  c.lp = dy * W + dx;
+  c.lv = slot0 * VS + c.lp;
+  c.lq = slot0 * QS - dy * a.S * a.K - dx * a.S;
+  c.GiVS = Gi * VS;
+  c.GiQS = Gi * QS;
+  c.oc_lane = oc0 + slot0;
+  c.r0 = r0; c.W = W; c.HW = a.HW; c.mql = a.mql;
+  c.ntab = qz.n_table;
+  int vtc[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) vtc[it] = vthc[min(it * Gi + slot0, Gp - 1)];
+
+  const int L = a.L;
+  const int nr = a.n_real[b];
+  const int n_eff = nr < 0 ? 0 : (nr < L ? nr : L);
+  const float* tb = a.times + (size_t)b * L;
+  const int32_t* sb = a.src + (size_t)b * L;
+
+  int vmin_l = 0, vmax_l = 0;
+  int out_base = 0;  // spikes emitted so far (wave 0, merge mode)
+
+  // Next chunk of events, loaded one chunk ahead.
+  int t_n = 0, s_n = -1;
+  if (lane < n_eff) { t_n = time_ms(tb[lane]); s_n = sb[lane]; }
+
+  for (int base = 0; base < n_eff; base += kWave) {
+    // ---- decode 64 events (connectivity/conv.py:15-43), one per lane
+    const int j = base + lane;
+    const int tv = t_n, sv = s_n;
+    {
+      const int j2 = j + kWave;
+      t_n = 0; s_n = -1;
+      if (j2 < n_eff) { t_n = time_ms(tb[j2]); s_n = sb[j2]; }
+    }
+    bool rel = j < n_eff && sv >= 0;
+    int ch = 0, y = 0, x = 0;
+    if (rel) {
+      ch = sv / a.HWin;
+      const int rem = sv - ch * a.HWin;
+      y = rem / a.Win;
+      x = rem - y * a.Win;
+      ch = min(ch, a.IC - 1);  // memory safety only; the host rejects such ids
+    }
+    // Candidate output rows [ceil((y+P-K+1)/S), floor((y+P)/S)] within [r0, r0+rn) and
+    // columns within [0, W) (connectivity/conv.py:15-29).
+    const int oy0 = floordiv_pos(y + a.P - a.K + a.S, a.S);
+    const int ox0 = floordiv_pos(x + a.P - a.K + a.S, a.S);
+    const int dyA = max(oy0, r0) - oy0, dyB = min((y + a.P) / a.S, r0 + rn - 1) - oy0;
+    const int dxA = max(ox0, 0) - ox0, dxB = min((x + a.P) / a.S, W - 1) - ox0;
+    rel = rel && dyA <= dyB && dxA <= dxB;
+    uint64_t m = 0;
+    if (rel) {
+      const uint64_t cols = (2ull << dxB) - (1ull << dxA);
+      for (int d = dyA; d <= dyB; ++d) m |= cols << (d * a.NC);
+    }
+    const int p0 = (oy0 - r0) * W + ox0;
+    const int q0 = ch * KK + (y + a.P - oy0 * a.S) * a.K + (x + a.P - ox0 * a.S);
+    const uint64_t relm = __ballot(rel);
+    const int n_ev = __popcll(relm);
+    if (rel) {
+      const int slot = lanes_below(relm);
+      c.rec[slot] = make_int4(tv, p0, q0, (int)(uint32_t)m);
+      c.rec1[slot] = make_int2((int)(uint32_t)(m >> 32), j);
+    }
+    if (a.merge)
+      for (int i = lane; i < kWave * NIT; i += kWave) c.stg[i] = 0;
+    __syncthreads();
+    if (a.merge) {
+      conv_events<NIT, F24, SAT, EXT, VTHN, true>(a, c, vtc, n_ev, b, vmin_l, vmax_l);
+      __syncthreads();  // every wave's ballots of this chunk are staged
+      if (wv == 0) {
+        // Walk (event, wave, iteration, bit) = (event, ascending neuron id).
+        const int e = lane;
+        int cnt = 0;
+        if (e < n_ev)
+          for (int w = 0; w < a.nw; ++w) {
+            const uint64_t* sg = reinterpret_cast<const uint64_t*>(
+                smem + lay.shared_words + w * lay.wave_words + lay.stg);
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) cnt += __popcll(sg[e * NIT + it]);
+          }
+        const int excl = wave_excl_scan(cnt, lane);
+        const int total = wave_sum(cnt);
+        if (cnt > 0) {
+          const int4 re = c.rec[e];
+          const float te = (float)re.x;
+          int pos = out_base + excl;
+          for (int w = 0; w < a.nw; ++w) {
+            const uint64_t* sg = reinterpret_cast<const uint64_t*>(
+                smem + lay.shared_words + w * lay.wave_words + lay.stg);
+            for (int it = 0; it < NIT; ++it) {
+              uint64_t bits = sg[e * NIT + it];
+              while (bits) {
+                const int k = __builtin_ctzll(bits);
+                bits &= bits - 1;
+                const int2 lmk = lanemap[k];
+                const int oc = w * a.G + it * Gi + lmk.x;
+                if (pos < a.cap) {
+                  a.out_t[(size_t)b * a.cap + pos] = te;
+                  a.out_s[(size_t)b * a.cap + pos] = oc * a.HW + re.y + lmk.y;
+                }
+                ++pos;
+              }
+            }
+          }
+        }
+        out_base += total;
+      }
+      __syncthreads();  // the staging and records are rewritten by the next chunk
+    } else {
+      conv_events<NIT, F24, SAT, EXT, VTHN, false>(a, c, vtc, n_ev, b, vmin_l, vmax_l);
+      __syncthreads();  // records are rewritten by the next chunk
+    }
+  }
+
+  // ---- catch-up column: decay to the last real input time T
+  // (connectivity/conv.py:102-125).  An empty position's catch-up has dt = 0; the
+  // identity columns after it repeat V.  A full queue has no catch-up column.
+  const int T = n_eff > 0 ? time_ms(tb[n_eff - 1]) : 0;
+  int maxcnt = 0;
+  for (int i = lane; i < PW; i += kWave) maxcnt = max(maxcnt, c.tc[i].y);
+  for (int li = lane; li < ocn * PW; li += kWave) {
+    const int s = li / PW;
+    const int p = li - s * PW;
+    const int2 st = c.tc[p];
+    const int vi = s * VS + p;
+    int32_t vv = c.Vs[vi];
+    int32_t mnn = EXT ? c.mn[vi] : 0, mxx = EXT ? c.mx[vi] : 0;
+    if (st.y < a.mql) {
+      const int dt = st.y > 0 ? T - st.x : 0;
+      vv = decay_mul<F24>(vv, c.ext[decay_slot(dt, c.ntab)], qz.fa, qz.rc);  // |D| <= |V|
+      vmin_l = min(vmin_l, vv);
+      vmax_l = max(vmax_l, vv);
+      mnn = min(mnn, vv);
+      mxx = max(mxx, vv);
+    }
+    const size_t ng = (size_t)b * (a.OC * a.HW) + (size_t)(oc0 + s) * a.HW + r0 * W + p;
+    if (a.v_final) a.v_final[ng] = vv;
+    if (EXT) {
+      a.v_min[ng] = mnn;
+      a.v_max[ng] = mxx;
+    }
+  }
+  vmin_l = wave_min(vmin_l);
+  vmax_l = wave_max(vmax_l);
+  maxcnt = wave_max(maxcnt);
+  if (lane == 0) {
+    red[wv * 4 + 0] = vmin_l;
+    red[wv * 4 + 1] = vmax_l;
+    red[wv * 4 + 2] = maxcnt;
+  }
+  __syncthreads();
+  if (wv != 0) return;
+  for (int w = 1; w < a.nw; ++w) {
+    vmin_l = min(vmin_l, red[w * 4 + 0]);
+    vmax_l = max(vmax_l, red[w * 4 + 1]);
+    maxcnt = max(maxcnt, red[w * 4 + 2]);
+  }
+  const int ovf = (vmin_l < -qz.half || vmax_l > qz.half - 1) ? 1 : 0;
+  if (a.merge) {
+    if (lane == 0) {
+      a.out_n[b] = out_base;
+      a.stats[b * 4 + 0] = vmin_l;
+      a.stats[b * 4 + 1] = vmax_l;
+      a.stats[b * 4 + 2] = maxcnt + 1;
+      a.stats[b * 4 + 3] = ovf;
+    }
+    if (a.fill_pads)
+      for (int i = min(out_base, a.cap) + lane; i < a.cap; i += kWave) {
+        a.out_t[(size_t)b * a.cap + i] = kPadTime;
+        a.out_s[(size_t)b * a.cap + i] = 0;
+      }
+  } else if (lane == 0) {
+    atomicMin(&a.stats[b * 4 + 0], vmin_l);
+    atomicMax(&a.stats[b * 4 + 1], vmax_l);
+    atomicMax(&a.stats[b * 4 + 2], maxcnt + 1);
+    atomicOr(&a.stats[b * 4 + 3], ovf);
+  }
+}
+
+}  // namespace salt

@@ -1,0 +1,50 @@
+// Launchers of the layer kernels.  Each kernel family is instantiated in its own
+// translation unit (conv_inst.hip once per iteration count, fc_inst.hip once per
+// weight width) so that the build compiles them in parallel.
+#pragma once
+
+#include "conv_kernel.hpp"
+#include "fc_kernel.hpp"
+
+namespace salt {
+
+constexpr int kLdsMax = 160 * 1024;  // gfx950 LDS per workgroup
+
+// Conv flags: bit 3 = 24-bit high multiply, bit 2 = saturate, bit 1 = per-neuron
+// extremes, bit 0 = per-neuron thresholds.
+enum : int { kConvF24 = 8, kConvSat = 4, kConvExt = 2, kConvVthN = 1 };
+
+// Iteration counts with an instantiated kernel family.
+#define SALT_CONV_NITS(X) X(1) X(2) X(3) X(4) X(8)
+#define SALT_DECLARE_CONV(N)                                                           \
+  hipError_t launch_conv_nit##N(const ConvArgs& a, int flags, dim3 grid, dim3 block,   \
+                                size_t lds, hipStream_t st);
+SALT_CONV_NITS(SALT_DECLARE_CONV)
+#undef SALT_DECLARE_CONV
+
+// FC flags: bit 2 = 24-bit high multiply, bit 1 = saturate, bit 0 = weights in LDS.
+enum : int { kFcF24 = 4, kFcSat = 2, kFcWlds = 1 };
+
+#define SALT_DECLARE_FC(B)                                                             \
+  hipError_t launch_fc_q##B(const FcArgs& a, int npl, int flags, dim3 grid, size_t lds, \
+                            hipStream_t st);
+SALT_DECLARE_FC(8)
+SALT_DECLARE_FC(16)
+SALT_DECLARE_FC(32)
+#undef SALT_DECLARE_FC
+
+// Sets the dynamic-LDS limit of a kernel once, then launches it.
+template <typename Args>
+hipError_t launch_with_lds(const void* kern, void (*fn)(Args), bool* attr_set, dim3 grid,
+                           dim3 block, size_t lds, hipStream_t st, const Args& a) {
+  if (!*attr_set) {
+    const hipError_t e =
+        hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+    if (e != hipSuccess) return e;
+    *attr_set = true;
+  }
+  hipLaunchKernelGGL(fn, grid, block, lds, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace salt

@@ -1,0 +1,111 @@
+// Device-side building blocks shared by the layer kernels of libsalt_hip.so
+// (gfx950, 64-lane wavefronts).  The fixed-point helpers restate
+// salt_core/quant/fixed_point.py and salt_core/quant/codes.py of the reference.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+
+#include "salt_hip.h"
+
+namespace salt {
+
+constexpr int kWave = 64;
+constexpr float kPadTime = 1e12f;  // salt_core/stream.py:13
+
+// Quantisation parameters of one layer, uniform over the launch.
+struct Quant {
+  int fa;        // shift_bits of the decay multiply (f_a)
+  int fV;        // fractional bits of the register (f_V)
+  int wbits;     // register width i_V + f_V
+  int rc;        // rounding constant: 2^(f_a-1) for round, 0 for truncate
+  int half;      // 2^(wbits-1)
+  int n_table;   // decay table entries (dt = 1 .. n_table)
+  int vth_kind;  // SALT_VTH_*
+  int vth_scalar;
+  const int32_t* vth;
+};
+
+// Decay multiply D = A*(V >> f_a) + ((A*(V & (2^f_a-1)) + c) >> f_a), which is the
+// split multiply of salt_core/quant/fixed_point.py:47-65 (bit-identical to
+// (A*V + c) >> f_a with an exact product).  A < 2^15 and the low part < 2^15, so the
+// low product is a 24-bit unsigned multiply-add; F24: the high part fits 24 bits too.
+template <bool F24>
+__device__ __forceinline__ int32_t decay_mul(int32_t v, int32_t a, int fa, int rc) {
+  const int32_t hi = v >> fa;
+  const uint32_t lo = (uint32_t)v & ((1u << fa) - 1u);
+  const int32_t t2 = (int32_t)((__umul24((uint32_t)a, lo) + (uint32_t)rc) >> fa);
+  return F24 ? __mul24(a, hi) + t2 : a * hi + t2;
+}
+
+// Write-back into the (i_V + f_V)-bit register, salt_core/quant/fixed_point.py:68-90:
+// saturate clamps, wrap keeps the low wbits bits sign-extended.
+template <bool SAT>
+__device__ __forceinline__ int32_t fit_bits(int32_t u, const Quant& qz) {
+  if (SAT) return min(max(u, -qz.half), qz.half - 1);
+  return __builtin_amdgcn_sbfe(u, 0, qz.wbits);
+}
+
+// Extended decay table in LDS: [0] = 2^f_a (dt = 0, the identity column, which the
+// decay multiply maps to V exactly), [1..n] = decay_table_int, [n+1] = 0 (dt > n).
+// Index = min(dt, n + 1): salt_core/quant/codes.py:87-105.
+__device__ __forceinline__ void load_ext_table(int32_t* ext, const int32_t* table,
+                                               int n_table, int fa, int lane, int nthreads) {
+  for (int i = lane; i < n_table + 2; i += nthreads)
+    ext[i] = i == 0 ? (1 << fa) : (i <= n_table ? table[i - 1] : 0);
+}
+
+// Times are float32 holding integer ms below 2^31 (checked on the host), so the
+// conversion is exact; the integer difference equals the reference's float32
+// difference wherever it selects a table entry (see the kernels' notes).
+__device__ __forceinline__ int time_ms(float t) { return (int)t; }
+
+__device__ __forceinline__ int decay_slot(int dt, int n_table) {
+  return min(max(dt, 0), n_table + 1);
+}
+
+__device__ __forceinline__ int floordiv_pos(int a, int s) {  // s > 0
+  return a >= 0 ? a / s : -((-a + s - 1) / s);
+}
+
+__device__ __forceinline__ int wave_min(int v) {
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ int wave_max(int v) {
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ int wave_sum(int v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+// Exclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ int wave_excl_scan(int v, int lane) {
+  int incl = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  return incl - v;
+}
+
+// Number of set bits of m below this lane (v_mbcnt).
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__device__ __forceinline__ int rdlane(int v, int lane) {
+  return __builtin_amdgcn_readlane(v, lane);
+}
+
+__device__ __forceinline__ int32_t load_code_bits(const void* p, size_t i, int bits) {
+  if (bits == 8) return (int32_t) static_cast<const int8_t*>(p)[i];
+  if (bits == 16) return (int32_t) static_cast<const int16_t*>(p)[i];
+  return static_cast<const int32_t*>(p)[i];
+}
+
+}  // namespace salt
