@@ -1,11 +1,13 @@
 // Event-driven integer conv layer (salt_core/layers/conv.py:124-149 with the queue of
 // salt_core/connectivity/conv.py and the scan of salt_core/quant/scan.py:22-132).
 //
-// A work-group owns one (stream, band of R output rows); its nw wavefronts split the
-// output channels (channel group = wave), and every wave consumes all of the stream's
-// events in order.  Everything a wave touches per event lives in LDS: registers
-// V[channel slot][position], per-position (last-update time, queue count), its weight
-// codes, and the shared extended decay table.
+// A work-group owns one stream and a band of R output rows (in-kernel output: the whole
+// plane).  Its waves split that band into ncg channel groups x nsb sub-bands of Rw rows;
+// every wave decodes all of the stream's events in order and processes those whose
+// candidate rows meet its sub-band.  Everything a wave touches per event lives in LDS:
+// registers V[channel slot][position], per-position (last-update time, queue count),
+// and -- shared by the waves of a channel group -- its weight codes and the extended
+// decay table.
 //
 // Lane mapping.  NC = (k-1)//s + 1 candidate rows (and columns) per input event and
 // NC2 = NC*NC candidates; lane l is channel slot l / NC2 (+ Gi per iteration) and
@@ -14,22 +16,23 @@
 // event-uniform base plus a lane constant:
 //   V slot    = ((oy0-r0)*W + ox0) + [slot*VS + dy*W + dx]
 //   weight    = (c*K*K + (y+P-oy0*S)*K + (x+P-ox0*S)) + [slot*QS - dy*S*K - dx*S]
-// (VS, QS: the odd per-slot strides of the register and weight arrays), so the
-// per-event loop does no index arithmetic beyond adds.  Each wave decodes 64 events at
-// a time (one per lane) into LDS records: those two bases, the time and a 64-bit mask
-// of the candidates inside the output plane and the band; the loop reads one record
-// per event (a broadcast LDS read).
+// (VS, QS: odd per-slot strides).  Each wave decodes 64 events at a time (one per lane)
+// into LDS records: those two bases, the time and a 64-bit mask of the candidates in
+// the output plane and its sub-band; the loop reads one record per event (a broadcast).
 //
-// Channel slots past a wave's channels hold zero weights and an unreachable
-// threshold: their registers stay 0, never fire and never move the extremes (which
-// start at 0), so no lane needs a per-iteration predicate.
+// No lane predicates in the event loop.  A lane without an update this event (no
+// candidate, or a full queue) reads and writes its own spare words, which hold zeros:
+// a zero register and a zero code give U = 0 and never fire, and the extremes start at
+// 0.  Channel slots past a wave's channels likewise hold zero codes and an unreachable
+// threshold.
 //
-// Output.  When the work-group holds the whole output plane (one band), each wave
-// stores the ballot of its spikes per (event, iteration) in LDS, and after every
-// 64-event chunk wave 0 walks them in (event, wave, iteration, lane) order -- which is
-// (event, ascending neuron id), the order of salt_core/stream.py:24-46 -- and appends
-// the spikes to the stream.  With several bands each wave sets per-event spike bits
-// in global memory instead, and a compaction kernel orders them.
+// Output.  With the whole plane in the work-group, each wave stores the ballot of its
+// spikes per (chunk event, iteration) in LDS; after each 64-event chunk wave 0 ORs the
+// sub-bands' ballots (same lane mapping, disjoint candidate rows) and walks (event,
+// channel group, iteration, lane) = (event, ascending neuron id) -- the order of
+// salt_core/stream.py:24-46 -- appending to the stream.  With several work-groups per
+// stream (state above the LDS size) each wave sets per-event spike bits in global
+// memory instead, and a compaction kernel orders them.
 //
 // No barrier inside the event loop: a wave's LDS operations complete in program
 // order, so event e+1 reads what event e wrote.
@@ -39,14 +42,14 @@
 
 namespace salt {
 
-constexpr int kConvMaxWaves = 8;  // channel groups (waves) per work-group
+constexpr int kConvMaxWaves = 8;  // waves per work-group
 
 struct ConvArgs {
   // geometry
   int IC, Win, HWin, OC, K, S, P, H, W, HW, NC, NC2, WPO, mql;
-  // partition: G channels per wave in NIT iterations of Gi slots, nw waves (channel
-  // groups) per work-group, R output rows per band
-  int G, Gi, nw, R;
+  // partition: G channels per channel group in NIT iterations of Gi slots; ncg channel
+  // groups x nsb sub-bands of Rw rows per work-group; R rows per work-group
+  int G, Gi, ncg, nsb, Rw, R;
   // quantisation
   Quant qz;
   const int32_t* table;
@@ -58,7 +61,7 @@ struct ConvArgs {
   const int32_t* src;
   const int32_t* n_real;
   // outputs
-  int cap, fill_pads, merge;  // merge: one band, ordered output written in-kernel
+  int cap, fill_pads, merge;  // merge: one work-group per stream, ordered output in-kernel
   float* out_t;
   int32_t* out_s;
   int32_t* out_n;
@@ -70,39 +73,41 @@ struct ConvArgs {
 };
 
 // LDS layout of a work-group, in 4-byte words: a shared part (decay table, ballot-bit
-// map, reduction slots), then one region per wave.
+// map, reduction slots, weight codes per channel group), then one region per wave.
 struct ConvLds {
-  int ext, lanemap, red, shared_words;                                // shared
-  int rec, rec1, stg, tc, vthc, qs, v, mn, mx, th, wave_words;        // per wave
-  int vs, qst;  // odd slot strides of the register and weight arrays
+  int ext, lanemap, red, qs, shared_words;                        // shared
+  int rec, rec1, stg, tc, vthc, v, mn, mx, th, wave_words;        // per wave
+  int vs, qst, tcn;  // slot strides (odd, with spare words), TC entries
   int words;
 };
 
-__host__ __device__ inline ConvLds conv_lds_layout(int n_table, int nw, int Gp, int nit,
-                                                   int ICKK, int PWs, bool ext, bool vthn) {
+__host__ __device__ inline ConvLds conv_lds_layout(int n_table, int ncg, int nsb, int Gp,
+                                                   int nit, int ICKK, int NC2, int PWs,
+                                                   bool ext, bool vthn) {
   ConvLds l;
-  l.vs = PWs | 1;
-  l.qst = ICKK | 1;
+  l.vs = (PWs + NC2) | 1;   // positions, then one spare word per candidate
+  l.qst = (ICKK + 1) | 1;   // codes, then at least one zero word
+  l.tcn = PWs + kWave;      // positions, then one spare entry per lane
   int o = 0;
   l.ext = o;     o += n_table + 2;
-  l.lanemap = o; o += 2 * kWave;               // int2 {slot, position offset} per lane
+  l.lanemap = o; o += 2 * kWave;  // int2 {slot, position offset} per ballot bit
   l.red = o;     o += 4 * kConvMaxWaves;
+  l.qs = o;      o += ncg * Gp * l.qst;
   o = (o + 3) & ~3;
   l.shared_words = o;
   int w = 0;
-  l.rec = w;  w += kWave * 4;     // int4 {t, V base, weight base, candidate mask low}
-  l.rec1 = w; w += kWave * 2;     // int2 {candidate mask high, event index}
-  l.stg = w;  w += kWave * nit * 2;  // uint64 spike ballot per (event, iteration)
-  l.tc = w;   w += 2 * PWs;       // int2 {last-update time, queue count} per position
+  l.rec = w;  w += kWave * 4;        // int4 {t, V base, weight base, candidate mask low}
+  l.rec1 = w; w += kWave * 2;        // int2 {candidate mask high, event index}
+  l.stg = w;  w += kWave * nit * 2;  // uint64 spike ballot per (chunk event, iteration)
+  l.tc = w;   w += 2 * l.tcn;        // int2 {last-update time, queue count}
   l.vthc = w; w += Gp;
-  l.qs = w;   w += Gp * l.qst;
   l.v = w;    w += Gp * l.vs;
   l.mn = w;   w += ext ? Gp * l.vs : 0;
   l.mx = w;   w += ext ? Gp * l.vs : 0;
   l.th = w;   w += vthn ? Gp * l.vs : 0;
   w = (w + 3) & ~3;
   l.wave_words = w;
-  l.words = l.shared_words + nw * w;
+  l.words = l.shared_words + ncg * nsb * w;
   return l;
 }
 
@@ -118,21 +123,27 @@ struct ConvLane {
   int32_t* mn;
   int32_t* mx;
   int32_t* th;
-  uint64_t lm;      // this lane's candidate bit (0 for lanes without a slot)
-  int first;        // slot 0: the lane that commits its position's time and count
-  int lp, lv, lq;   // position / register / weight offsets relative to an event's bases
+  uint64_t lm;          // this lane's candidate bit (0 for lanes without a slot)
+  int first;            // slot 0: the lane that commits its position's time and count
+  int lp, lv, lq;       // position / register / code offsets relative to an event's bases
+  int v_spare, q_zero, tc_spare;  // this lane's spare register word, zero code, spare entry
   int GiVS, GiQS;
-  int cand, oc_lane, r0, W, HW, mql, ntab;
+  int cand, oc_lane, mql, ntab;
 };
 
 // The events of one decoded chunk, in order (salt_core/quant/scan.py:22-52 per update).
-// MERGE: stage the spike ballots for the work-group's merge; otherwise set the
-// partition's spike bits in global memory.
+// MERGE: stage the spike ballots for the work-group's merge; otherwise set spike bits
+// in global memory.
 template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, bool MERGE>
 __device__ __forceinline__ void conv_events(const ConvArgs& a, const ConvLane& c,
-                                            const int (&vtc)[NIT], int n_ev, int b,
+                                            const int (&vtc)[NIT], int n_ev, int base, int b,
                                             int& vmin_l, int& vmax_l) {
   if (n_ev == 0) return;
+  // MERGE: lane e of sg_lo/sg_hi[it] collects event e's spike ballot; they are
+  // stored once per chunk.
+  uint32_t sg_lo[NIT], sg_hi[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) { sg_lo[it] = 0; sg_hi[it] = 0; }
   const Quant& qz = a.qz;
   const int fa = qz.fa, rc = qz.rc;
   const int lane = threadIdx.x & (kWave - 1);
@@ -142,64 +153,53 @@ __device__ __forceinline__ void conv_events(const ConvArgs& a, const ConvLane& c
   int4 r = c.rec[0];
   int2 r1 = c.rec1[0];
   bool vc = ((((uint64_t)(uint32_t)r1.x << 32) | (uint32_t)r.w) & c.lm) != 0;
-  int pa = r.y + c.lp;
-  int2 st = make_int2(0, 0);
-  if (vc) st = c.tc[pa];
+  int2 st = c.tc[vc ? r.y + c.lp : c.tc_spare];
   for (int e = 0; e < n_ev; ++e) {
     const bool more = e + 1 < n_ev;
     const int4 rn = c.rec[more ? e + 1 : e];
     const int2 rn1 = c.rec1[more ? e + 1 : e];
-    int fire[NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) fire[it] = 0;
+    const int pa = r.y + c.lp;
     // A position whose queue is full (max_queue_len real columns) drops the event and
     // its time (connectivity/conv.py:57-99 truncates the queue).
     const bool act = vc && st.y < c.mql;
-    int A = 0;
+    c.tc[(vc && c.first) ? pa : c.tc_spare] = make_int2(act ? r.x : st.x, st.y + 1);
+    const int A = c.ext[decay_slot(r.x - st.x, c.ntab)];
+    const int va = act ? r.y + c.lv : c.v_spare;
+    const int qa = act ? r.z + c.lq : c.q_zero;
     int v[NIT], qv[NIT], vt[NIT], mnv[NIT], mxv[NIT];
-    const int va = r.y + c.lv, qa = r.z + c.lq;
-    if (vc) {
-      if (c.first) c.tc[pa] = make_int2(act ? r.x : st.x, st.y + 1);
-      if (act) {
-        A = c.ext[decay_slot(r.x - st.x, c.ntab)];
-#pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-          v[it] = c.Vs[va + it * c.GiVS];
-          qv[it] = c.qs[qa + it * c.GiQS];
-          vt[it] = VTHN ? c.th[va + it * c.GiVS] : vtc[it];
-          if (EXT) { mnv[it] = c.mn[va + it * c.GiVS]; mxv[it] = c.mx[va + it * c.GiVS]; }
-        }
-      }
-    }
-    const bool vcn = more && ((((uint64_t)(uint32_t)rn1.x << 32) | (uint32_t)rn.w) & c.lm) != 0;
-    const int pan = rn.y + c.lp;
-    int2 stn = make_int2(0, 0);
-    if (vcn) stn = c.tc[pan];
-    if (act) {
-#pragma unroll
-      for (int it = 0; it < NIT; ++it) {
-        const int32_t d = decay_mul<F24>(v[it], A, fa, rc);
-        const int32_t u = (int32_t)((uint32_t)d + (uint32_t)qv[it]);  // codes hold q*2^f_V
-        const int32_t f = fit_bits<SAT>(u, qz);
-        const bool fi = f >= vt[it];
-        fire[it] = fi ? 1 : 0;
-        c.Vs[va + it * c.GiVS] = fi ? 0 : f;
-        vmin_l = min(vmin_l, u);
-        vmax_l = max(vmax_l, u);
-        if (EXT) {
-          c.mn[va + it * c.GiVS] = min(mnv[it], u);
-          c.mx[va + it * c.GiVS] = max(mxv[it], u);
-        }
-      }
-    }
-    // Spikes, in uniform control flow.
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-      const uint64_t bal = __ballot(fire[it] != 0);
-      if (bal) {
-        if (MERGE) {
-          if (lane == 0) c.stg[e * NIT + it] = bal;
-        } else if (fire[it]) {
+      v[it] = c.Vs[va + it * c.GiVS];
+      qv[it] = c.qs[qa + it * c.GiQS];
+      vt[it] = VTHN ? c.th[va + it * c.GiVS] : vtc[it];
+      if (EXT) { mnv[it] = c.mn[va + it * c.GiVS]; mxv[it] = c.mx[va + it * c.GiVS]; }
+    }
+    const bool vcn = more && ((((uint64_t)(uint32_t)rn1.x << 32) | (uint32_t)rn.w) & c.lm) != 0;
+    const int2 stn = c.tc[vcn ? rn.y + c.lp : c.tc_spare];
+    uint64_t bal[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int32_t d = decay_mul<F24>(v[it], A, fa, rc);
+      const int32_t u = (int32_t)((uint32_t)d + (uint32_t)qv[it]);  // codes hold q*2^f_V
+      const int32_t f = fit_bits<SAT>(u, qz);
+      const bool fi = f >= vt[it];
+      c.Vs[va + it * c.GiVS] = fi ? 0 : f;
+      vmin_l = min(vmin_l, u);
+      vmax_l = max(vmax_l, u);
+      if (EXT) {
+        c.mn[va + it * c.GiVS] = min(mnv[it], u);
+        c.mx[va + it * c.GiVS] = max(mxv[it], u);
+      }
+      bal[it] = __ballot(fi);
+    }
+    const bool mine = lane == e;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      if (MERGE) {
+        sg_lo[it] = mine ? (uint32_t)bal[it] : sg_lo[it];
+        sg_hi[it] = mine ? (uint32_t)(bal[it] >> 32) : sg_hi[it];
+      } else if (bal[it]) {
+        if ((bal[it] >> lane) & 1) {
           // Bit = candidate index in the event's NC x NC grid (compaction decodes it).
           const size_t w = ((size_t)b * a.L + r1.y) * (size_t)(a.OC * a.WPO) +
                            (size_t)(c.oc_lane + it * a.Gi) * a.WPO + (c.cand >> 5);
@@ -210,9 +210,14 @@ __device__ __forceinline__ void conv_events(const ConvArgs& a, const ConvLane& c
     r = rn;
     r1 = rn1;
     vc = vcn;
-    pa = pan;
     st = stn;
     asm volatile("" ::: "memory");  // keep this event's LDS traffic before the next one's
+  }
+  if (MERGE && lane < n_ev) {
+    const int jc = c.rec1[lane].y - base;  // the event's index within the chunk
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+      c.stg[jc * NIT + it] = ((uint64_t)sg_hi[it] << 32) | sg_lo[it];
   }
 }
 
@@ -221,41 +226,53 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   extern __shared__ int32_t smem[];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);  // channel group
+  const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int nthr = blockDim.x;
   const int b = blockIdx.y;
-  const int rb = blockIdx.x;   // band
+  const int cg = wv % a.ncg, sb = wv / a.ncg;  // channel group, sub-band
   const int Gi = a.Gi, Gp = NIT * a.Gi;
-  const int oc0 = wv * a.G;
+  const int oc0 = cg * a.G;
   const int ocn = max(0, min(a.G, a.OC - oc0));
-  const int r0 = rb * a.R;
-  const int rn = min(a.R, a.H - r0);
-  const int W = a.W, PWs = a.R * W, PW = rn * W;
+  const int rows_end = min(a.H, (int)blockIdx.x * a.R + a.R);
+  const int r0 = blockIdx.x * a.R + sb * a.Rw;
+  const int rn = max(0, min(a.Rw, rows_end - r0));
+  const int W = a.W, PWs = a.Rw * W, PW = rn * W;
   const int KK = a.K * a.K, ICKK = a.IC * KK;
   const Quant& qz = a.qz;
-  const ConvLds lay = conv_lds_layout(qz.n_table, a.nw, Gp, NIT, ICKK, PWs, EXT, VTHN);
+  const ConvLds lay = conv_lds_layout(qz.n_table, a.ncg, a.nsb, Gp, NIT, ICKK, a.NC2, PWs,
+                                      EXT, VTHN);
+  const int VS = lay.vs, QS = lay.qst;
   int32_t* wbase = smem + lay.shared_words + wv * lay.wave_words;
   int2* lanemap = reinterpret_cast<int2*>(smem + lay.lanemap);
   int32_t* red = smem + lay.red;
   ConvLane c;
   c.ext = smem + lay.ext;
+  c.qs = smem + lay.qs + cg * Gp * QS;
   c.rec = reinterpret_cast<int4*>(wbase + lay.rec);
   c.rec1 = reinterpret_cast<int2*>(wbase + lay.rec1);
   c.stg = reinterpret_cast<uint64_t*>(wbase + lay.stg);
   c.tc = reinterpret_cast<int2*>(wbase + lay.tc);
   int32_t* vthc = wbase + lay.vthc;
-  c.qs = wbase + lay.qs;
   c.Vs = wbase + lay.v;
   c.mn = wbase + lay.mn;
   c.mx = wbase + lay.mx;
   c.th = wbase + lay.th;
-  const int VS = lay.vs, QS = lay.qst;
 
-  // ---- shared state: decay table, ballot bit -> (slot, position offset)
+  // ---- shared state: decay table, ballot bit -> (slot, position offset), codes
   load_ext_table(c.ext, a.table, qz.n_table, qz.fa, tid, nthr);
   for (int k = tid; k < kWave; k += nthr) {
     const int s = k / a.NC2, cd = k - s * a.NC2;
     lanemap[k] = make_int2(s, (cd / a.NC) * W + (cd - (cd / a.NC) * a.NC));
+  }
+  for (int i = tid; i < a.ncg * Gp * QS; i += nthr) {
+    const int g = i / (Gp * QS), rem = i - g * (Gp * QS);
+    const int s = rem / QS, k = rem - s * QS;
+    const int oc = g * a.G + s;
+    // Codes are stored pre-shifted, q * 2^f_V in two's complement (U = D + q*2^f_V).
+    smem[lay.qs + i] = (s < a.G && oc < a.OC && k < ICKK)
+                           ? (int32_t)((uint32_t)load_code_bits(a.q, (size_t)oc * ICKK + k,
+                                                                a.q_bits) << qz.fV)
+                           : 0;
   }
   // ---- this wave's state
   for (int i = lane; i < Gp; i += kWave) {
@@ -266,14 +283,6 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
     }
     vthc[i] = v;
   }
-  for (int i = lane; i < Gp * QS; i += kWave) {
-    const int s = i / QS, k = i - s * QS;
-    // Codes are stored pre-shifted: q * 2^f_V in two's complement, as U = D + q*2^f_V.
-    c.qs[i] = (s < ocn && k < ICKK)
-                  ? (int32_t)((uint32_t)load_code_bits(a.q, (size_t)(oc0 + s) * ICKK + k,
-                                                       a.q_bits) << qz.fV)
-                  : 0;
-  }
   for (int i = lane; i < Gp * VS; i += kWave) {
     c.Vs[i] = 0;
     if (EXT) { c.mn[i] = 0; c.mx[i] = 0; }
@@ -282,7 +291,7 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
       c.th[i] = (s < ocn && p < PW) ? qz.vth[(size_t)(oc0 + s) * a.HW + r0 * W + p] : INT_MAX;
     }
   }
-  for (int i = lane; i < PWs; i += kWave) c.tc[i] = make_int2(0, 0);
+  for (int i = lane; i < lay.tcn; i += kWave) c.tc[i] = make_int2(0, 0);
   __syncthreads();
 
   // ---- lane constants
@@ -290,15 +299,19 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   c.cand = lane - slot0 * a.NC2;
   const int dy = c.cand / a.NC, dx = c.cand - (c.cand / a.NC) * a.NC;
   const bool lane_on = slot0 < Gi;
+  const int slot_t = lane_on ? slot0 : 0;
   c.lm = lane_on ? (1ull << c.cand) : 0ull;
   c.first = (lane_on && slot0 == 0) ? 1 : 0;
   c.lp = dy * W + dx;
   c.lv = slot0 * VS + c.lp;
   c.lq = slot0 * QS - dy * a.S * a.K - dx * a.S;
+  c.v_spare = slot_t * VS + PWs + c.cand;
+  c.q_zero = slot_t * QS + ICKK;
+  c.tc_spare = PWs + lane;
   c.GiVS = Gi * VS;
   c.GiQS = Gi * QS;
   c.oc_lane = oc0 + slot0;
-  c.r0 = r0; c.W = W; c.HW = a.HW; c.mql = a.mql;
+  c.mql = a.mql;
   c.ntab = qz.n_table;
   int vtc[NIT];
 #pragma unroll
@@ -308,14 +321,14 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   const int nr = a.n_real[b];
   const int n_eff = nr < 0 ? 0 : (nr < L ? nr : L);
   const float* tb = a.times + (size_t)b * L;
-  const int32_t* sb = a.src + (size_t)b * L;
+  const int32_t* sb_src = a.src + (size_t)b * L;
 
   int vmin_l = 0, vmax_l = 0;
   int out_base = 0;  // spikes emitted so far (wave 0, merge mode)
 
   // Next chunk of events, loaded one chunk ahead.
   int t_n = 0, s_n = -1;
-  if (lane < n_eff) { t_n = time_ms(tb[lane]); s_n = sb[lane]; }
+  if (lane < n_eff) { t_n = time_ms(tb[lane]); s_n = sb_src[lane]; }
 
   for (int base = 0; base < n_eff; base += kWave) {
     // ---- decode 64 events (connectivity/conv.py:15-43), one per lane
@@ -324,11 +337,11 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
     {
       const int j2 = j + kWave;
       t_n = 0; s_n = -1;
-      if (j2 < n_eff) { t_n = time_ms(tb[j2]); s_n = sb[j2]; }
+      if (j2 < n_eff) { t_n = time_ms(tb[j2]); s_n = sb_src[j2]; }
     }
-    bool rel = j < n_eff && sv >= 0;
+    const bool real = j < n_eff && sv >= 0;
     int ch = 0, y = 0, x = 0;
-    if (rel) {
+    if (real) {
       ch = sv / a.HWin;
       const int rem = sv - ch * a.HWin;
       y = rem / a.Win;
@@ -341,7 +354,7 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
     const int ox0 = floordiv_pos(x + a.P - a.K + a.S, a.S);
     const int dyA = max(oy0, r0) - oy0, dyB = min((y + a.P) / a.S, r0 + rn - 1) - oy0;
     const int dxA = max(ox0, 0) - ox0, dxB = min((x + a.P) / a.S, W - 1) - ox0;
-    rel = rel && dyA <= dyB && dxA <= dxB;
+    const bool rel = real && dyA <= dyB && dxA <= dxB;
     uint64_t m = 0;
     if (rel) {
       const uint64_t cols = (2ull << dxB) - (1ull << dxA);
@@ -360,49 +373,51 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
       for (int i = lane; i < kWave * NIT; i += kWave) c.stg[i] = 0;
     __syncthreads();
     if (a.merge) {
-      conv_events<NIT, F24, SAT, EXT, VTHN, true>(a, c, vtc, n_ev, b, vmin_l, vmax_l);
+      conv_events<NIT, F24, SAT, EXT, VTHN, true>(a, c, vtc, n_ev, base, b, vmin_l, vmax_l);
       __syncthreads();  // every wave's ballots of this chunk are staged
       if (wv == 0) {
-        // Walk (event, wave, iteration, bit) = (event, ascending neuron id).
-        const int e = lane;
+        // Walk (event, channel group, iteration, bit) = (event, ascending neuron id);
+        // the sub-bands' ballots of one event are disjoint and share the lane mapping.
+        const int nw = a.ncg * a.nsb;
         int cnt = 0;
-        if (e < n_ev)
-          for (int w = 0; w < a.nw; ++w) {
-            const uint64_t* sg = reinterpret_cast<const uint64_t*>(
-                smem + lay.shared_words + w * lay.wave_words + lay.stg);
-#pragma unroll
-            for (int it = 0; it < NIT; ++it) cnt += __popcll(sg[e * NIT + it]);
+        for (int g = 0; g < a.ncg; ++g)
+          for (int it = 0; it < NIT; ++it) {
+            uint64_t bits = 0;
+            for (int w = g; w < nw; w += a.ncg)
+              bits |= reinterpret_cast<const uint64_t*>(
+                  smem + lay.shared_words + w * lay.wave_words + lay.stg)[lane * NIT + it];
+            cnt += __popcll(bits);
           }
         const int excl = wave_excl_scan(cnt, lane);
         const int total = wave_sum(cnt);
         if (cnt > 0) {
-          const int4 re = c.rec[e];
-          const float te = (float)re.x;
+          const float te = (float)tv;
+          const int pg = oy0 * W + ox0;  // plane position of the event's first candidate
           int pos = out_base + excl;
-          for (int w = 0; w < a.nw; ++w) {
-            const uint64_t* sg = reinterpret_cast<const uint64_t*>(
-                smem + lay.shared_words + w * lay.wave_words + lay.stg);
+          for (int g = 0; g < a.ncg; ++g)
             for (int it = 0; it < NIT; ++it) {
-              uint64_t bits = sg[e * NIT + it];
+              uint64_t bits = 0;
+              for (int w = g; w < nw; w += a.ncg)
+                bits |= reinterpret_cast<const uint64_t*>(
+                    smem + lay.shared_words + w * lay.wave_words + lay.stg)[lane * NIT + it];
               while (bits) {
                 const int k = __builtin_ctzll(bits);
                 bits &= bits - 1;
                 const int2 lmk = lanemap[k];
-                const int oc = w * a.G + it * Gi + lmk.x;
+                const int oc = g * a.G + it * Gi + lmk.x;
                 if (pos < a.cap) {
                   a.out_t[(size_t)b * a.cap + pos] = te;
-                  a.out_s[(size_t)b * a.cap + pos] = oc * a.HW + re.y + lmk.y;
+                  a.out_s[(size_t)b * a.cap + pos] = oc * a.HW + pg + lmk.y;
                 }
                 ++pos;
               }
             }
-          }
         }
         out_base += total;
       }
       __syncthreads();  // the staging and records are rewritten by the next chunk
     } else {
-      conv_events<NIT, F24, SAT, EXT, VTHN, false>(a, c, vtc, n_ev, b, vmin_l, vmax_l);
+      conv_events<NIT, F24, SAT, EXT, VTHN, false>(a, c, vtc, n_ev, base, b, vmin_l, vmax_l);
       __syncthreads();  // records are rewritten by the next chunk
     }
   }
@@ -445,7 +460,7 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   }
   __syncthreads();
   if (wv != 0) return;
-  for (int w = 1; w < a.nw; ++w) {
+  for (int w = 1; w < a.ncg * a.nsb; ++w) {
     vmin_l = min(vmin_l, red[w * 4 + 0]);
     vmax_l = max(vmax_l, red[w * 4 + 1]);
     maxcnt = max(maxcnt, red[w * 4 + 2]);

@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -188,7 +189,7 @@ __global__ void transpose_kernel(const T* in, T* out, int n_out, int n_in) {
 // ------------------------------------------------------------------ planning
 
 struct ConvPlan {
-  int H, W, HW, NC, NC2, WPO, Gi, G, nit, nw, R, n_rb, merge;
+  int H, W, HW, NC, NC2, WPO, Gi, G, nit, ncg, nsb, Rw, R, n_rb, merge;
   size_t lds;
 };
 
@@ -197,18 +198,43 @@ int round_nit(int n) {  // smallest instantiated iteration count >= n
   return n <= 8 ? 8 : -1;
 }
 
-size_t conv_lds_bytes(const salt_layer_desc* d, const salt_qparams* p, int nw, int nit, int Gi,
-                      int R, int W, bool ext) {
-  const ConvLds l = conv_lds_layout(p->n_table, nw, nit * Gi, nit, d->ic * d->k * d->k, R * W,
-                                    ext, p->v_th_kind == SALT_VTH_PER_NEURON);
+size_t conv_lds_bytes(const salt_layer_desc* d, const salt_qparams* p, const ConvPlan& pl,
+                      bool ext) {
+  const ConvLds l = conv_lds_layout(p->n_table, pl.ncg, pl.nsb, pl.nit * pl.Gi, pl.nit,
+                                    d->ic * d->k * d->k, pl.NC2, pl.Rw * pl.W, ext,
+                                    p->v_th_kind == SALT_VTH_PER_NEURON);
   return (size_t)l.words * 4;
 }
 
-// Chooses the partition of a conv layer: channel groups of G channels (one wave each,
-// NIT iterations of Gi channel slots per event), as many waves per stream as fit
-// (<= 8, fewest iterations first), all in one work-group that holds the whole output
-// plane when its LDS fits; otherwise bands of R output rows, one work-group each.
-int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, bool ext, ConvPlan* pl) {
+// Fills the channel split of a plan: ncg channel groups of G channels, nit iterations
+// of Gi slots per event, the fewest iterations whose group count fits max_cg.
+bool split_channels(int OC, int max_cg, ConvPlan* pl) {
+  for (int nit = 1; nit <= 8; nit = nit < 4 ? nit + 1 : 8 + (nit == 8)) {
+    const int ncg = (OC + nit * pl->Gi - 1) / (nit * pl->Gi);
+    if (ncg > max_cg) continue;
+    pl->ncg = ncg;
+    pl->G = (OC + ncg - 1) / ncg;                       // balanced groups
+    pl->nit = round_nit((pl->G + pl->Gi - 1) / pl->Gi);
+    return true;
+  }
+  return false;
+}
+
+// Optional override for tuning runs: SALT_CONV_PLAN="ncg_max,nsb" (channel-group limit,
+// sub-bands per work-group).  Unset in normal use.
+bool plan_override(int* ncg_max, int* nsb) {
+  const char* e = getenv("SALT_CONV_PLAN");
+  return e && sscanf(e, "%d,%d", ncg_max, nsb) == 2 && *ncg_max >= 1 && *nsb >= 1;
+}
+
+// Chooses the partition of a conv layer.  One work-group per stream holds the whole
+// output plane whenever its LDS fits; its waves are channel groups, each with one
+// iteration per event where 8 waves suffice (a lone wave per SIMD is latency-bound,
+// and channel groups see the same events, so they stay in step between the per-chunk
+// barriers; row sub-bands are supported but unbalanced for clustered events).
+// Otherwise several work-groups per stream each take a band of rows.
+int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext,
+                  ConvPlan* pl) {
   pl->H = (d->h_in + 2 * d->p - d->k) / d->s + 1;
   pl->W = (d->w_in + 2 * d->p - d->k) / d->s + 1;
   if (pl->H < 1 || pl->W < 1) return fail(-1, "conv geometry gives an empty output plane");
@@ -220,33 +246,29 @@ int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, bool ext, Con
                 d->k, d->s);
   pl->WPO = (pl->NC2 + 31) / 32;
   pl->Gi = kWave / pl->NC2;
-  const int H = pl->H, W = pl->W, OC = d->oc, Gi = pl->Gi;
-  int first_nit = -1;
-  for (int nit = 1; nit > 0 && nit <= 8; nit = (nit < 4 ? nit + 1 : (nit == 4 ? 8 : -1))) {
-    const int nw = (OC + nit * Gi - 1) / (nit * Gi);
-    if (nw > kConvMaxWaves) continue;
-    const int G = (OC + nw - 1) / nw;                 // balanced channel groups
-    const int nit_g = round_nit((G + Gi - 1) / Gi);
-    if (first_nit < 0) first_nit = nit_g;
-    const size_t lds = conv_lds_bytes(d, p, nw, nit_g, Gi, H, W, ext);
-    if (lds <= (size_t)kLdsMax) {
-      pl->G = G; pl->nit = nit_g; pl->nw = nw; pl->R = H; pl->n_rb = 1; pl->merge = 1;
-      pl->lds = lds;
-      return 0;
-    }
-  }
-  if (first_nit < 0) return fail(-3, "conv: %d output channels need more than 8 iterations", OC);
-  // Bands: the fewest iterations per event, rows until the work-group fits the budget.
-  const int nw = (OC + first_nit * Gi - 1) / (first_nit * Gi);
-  const int G = (OC + nw - 1) / nw;
-  const int nit = round_nit((G + Gi - 1) / Gi);
+  const int H = pl->H, OC = d->oc;
+  int ncg_max = kConvMaxWaves, nsb = 1;
+  plan_override(&ncg_max, &nsb);
+  if (!split_channels(OC, ncg_max, pl) && !split_channels(OC, kConvMaxWaves, pl))
+    return fail(-3, "conv: %d output channels need more than 8 iterations", OC);
+  nsb = std::max(1, std::min(nsb, kConvMaxWaves / pl->ncg));
+  pl->Rw = (H + nsb - 1) / nsb;
+  pl->nsb = (H + pl->Rw - 1) / pl->Rw;                // no empty sub-band
+  pl->R = H; pl->n_rb = 1; pl->merge = 1;
+  pl->lds = conv_lds_bytes(d, p, *pl, ext);
+  if (pl->lds <= (size_t)kLdsMax) return 0;
+  // Bands of rows, one work-group (of channel-group waves) each, within the budget.
+  pl->nsb = 1; pl->merge = 0;
   int R = H;
-  while (R > 1 && conv_lds_bytes(d, p, nw, nit, Gi, R, W, ext) > (size_t)kLdsBandBudget) --R;
-  const size_t lds = conv_lds_bytes(d, p, nw, nit, Gi, R, W, ext);
-  if (lds > (size_t)kLdsMax) return fail(-3, "conv: one output row does not fit in LDS (w_out=%d)", W);
-  pl->G = G; pl->nit = nit; pl->nw = nw; pl->R = R; pl->n_rb = (H + R - 1) / R;
-  pl->merge = pl->n_rb == 1;
-  pl->lds = lds;
+  for (;;) {
+    pl->Rw = pl->R = R;
+    pl->lds = conv_lds_bytes(d, p, *pl, ext);
+    if (pl->lds <= (size_t)kLdsBandBudget || R == 1) break;
+    --R;
+  }
+  if (pl->lds > (size_t)kLdsMax)
+    return fail(-3, "conv: one output row does not fit in LDS (w_out=%d)", pl->W);
+  pl->n_rb = (H + R - 1) / R;
   return 0;
 }
 
@@ -335,7 +357,7 @@ int32_t fill(int32_t* p, int32_t v, size_t n, hipStream_t st) {
 
 hipError_t launch_conv(const ConvArgs& a, const ConvPlan& pl, int flags, int B,
                        hipStream_t st) {
-  const dim3 grid(pl.n_rb, B), block(kWave * pl.nw);
+  const dim3 grid(pl.n_rb, B), block(kWave * pl.ncg * pl.nsb);
   switch (pl.nit) {
 #define SALT_CASE(N) \
     case N: return launch_conv_nit##N(a, flags, grid, block, pl.lds, st);
@@ -416,7 +438,7 @@ int32_t salt_layer_workspace_size(const salt_layer_desc* desc, const salt_qparam
   if (!bytes || B < 0 || L < 0) return fail(-1, "invalid batch shape");
   if (desc->kind == SALT_LAYER_CONV) {
     ConvPlan pl;
-    rc = plan_conv(desc, prm, want_neuron_extremes != 0, &pl);
+    rc = plan_conv(desc, prm, B, want_neuron_extremes != 0, &pl);
     if (rc) return rc;
     *bytes = mask_bytes_conv(pl, desc, B, L);
   } else {
@@ -454,7 +476,7 @@ int32_t salt_layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
 
   if (desc->kind == SALT_LAYER_CONV) {
     ConvPlan pl;
-    rc = plan_conv(desc, prm, ext, &pl);
+    rc = plan_conv(desc, prm, B, ext, &pl);
     if (rc) return rc;
     const size_t need = mask_bytes_conv(pl, desc, B, L);
     if (workspace_bytes < need || (need && !d_workspace))
@@ -464,7 +486,7 @@ int32_t salt_layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     a.OC = desc->oc; a.K = desc->k; a.S = desc->s; a.P = desc->p;
     a.H = pl.H; a.W = pl.W; a.HW = pl.HW; a.NC = pl.NC; a.NC2 = pl.NC2; a.WPO = pl.WPO;
     a.mql = desc->max_queue_len;
-    a.G = pl.G; a.Gi = pl.Gi; a.nw = pl.nw; a.R = pl.R;
+    a.G = pl.G; a.Gi = pl.Gi; a.ncg = pl.ncg; a.nsb = pl.nsb; a.Rw = pl.Rw; a.R = pl.R;
     a.qz = qz; a.table = prm->d_decay_table; a.q = prm->d_q; a.q_bits = prm->q_bits;
     a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
     a.cap = out->cap; a.fill_pads = out->fill_pads; a.merge = pl.merge;

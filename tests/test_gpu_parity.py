@@ -129,3 +129,25 @@ def test_repeat_runs_are_bitwise_identical():
     b = run_layer(layer, params, times, src, n_real, round_mode=rm)
     assert bool((a.stream.event_source_idx == b.stream.event_source_idx).all())
     assert bool((a.result.v_final == b.result.v_final).all())
+
+
+@pytest.mark.parametrize("plan", ["1,2", "1,3", "2,2", "1,8"])
+def test_conv_work_group_shapes_match_oracle(plan, monkeypatch):
+    """Every work-group shape the planner can choose (channel groups x row sub-bands,
+    forced through SALT_CONV_PLAN) gives the oracle's streams, registers and extremes."""
+    monkeypatch.setenv("SALT_CONV_PLAN", plan)
+    for mi, case in enumerate([(2, 34, 34, 16, 5, 2, 0, 8, 400), (16, 15, 15, 32, 3, 2, 0, 8, 400),
+                               (2, 12, 12, 8, 3, 1, 1, 8, 300)]):
+        ic, h, w, oc, k, s, p, B, L = case
+        rng = np.random.default_rng(77 + mi)
+        layer = ConvLayer(name="c", ic=ic, h_in=h, w_in=w, oc=oc, k=k, s=s, p=p, init_k=1.0,
+                          max_queue_len=int(rng.choice([L + 1, max(2, L // 20)])),
+                          max_out_spikes=4 * L * oc)
+        params, rm = _params(rng, layer.weight_shape, layer.n_neurons, oc, MODES[mi], 8,
+                             ["scalar", "neuron", "channel"][mi])
+        times, src, n_real = _events(rng, B, L, ic * h * w)
+        print("plan", plan, "case", case, flush=True)
+        out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+        geom, prm, cap = oracle_spec(layer, params, rm)
+        ref = O.layer_forward(geom, prm, times, src, n_real, cap)
+        assert_layer_equal(out, ref, tag=f"{plan} {case}")
