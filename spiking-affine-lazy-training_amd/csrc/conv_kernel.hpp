@@ -32,7 +32,8 @@
 // channel group, iteration, lane) = (event, ascending neuron id) -- the order of
 // salt_core/stream.py:24-46 -- appending to the stream.  With several work-groups per
 // stream (state above the LDS size) each wave sets per-event spike bits in global
-// memory instead, and a compaction kernel orders them.
+// memory instead, and a compaction kernel orders them.  A wave that holds a whole
+// layer (the fused network kernel) appends its spikes to the stream itself.
 //
 // No barrier inside the event loop: a wave's LDS operations complete in program
 // order, so event e+1 reads what event e wrote.
@@ -44,9 +45,14 @@ namespace salt {
 
 constexpr int kConvMaxWaves = 8;  // waves per work-group
 
+// Geometry of a conv layer as the device code uses it.
+struct ConvGeom {
+  int IC, Win, HWin, OC, K, S, P, H, W, HW, NC, NC2, mql;
+};
+
 struct ConvArgs {
-  // geometry
-  int IC, Win, HWin, OC, K, S, P, H, W, HW, NC, NC2, WPO, mql;
+  ConvGeom g;
+  int WPO;  // spike-mask words per (event, channel)
   // partition: G channels per channel group in NIT iterations of Gi slots; ncg channel
   // groups x nsb sub-bands of Rw rows per work-group; R rows per work-group
   int G, Gi, ncg, nsb, Rw, R;
@@ -72,12 +78,29 @@ struct ConvArgs {
   uint32_t* masks;
 };
 
-// LDS layout of a work-group, in 4-byte words: a shared part (decay table, ballot-bit
-// map, reduction slots, weight codes per channel group), then one region per wave.
+// Odd slot strides with spare words, and the size of the per-position array.
+__host__ __device__ inline int conv_vs(int PWs, int NC2) { return (PWs + NC2) | 1; }
+__host__ __device__ inline int conv_qs(int ICKK) { return (ICKK + 1) | 1; }
+__host__ __device__ inline int conv_tcn(int PWs) { return PWs + kWave; }
+
+// LDS words of one wave's private state: records, staged ballots (nit per event when
+// stg), per-position (time, count), thresholds, registers and optional extremes /
+// per-neuron thresholds.  Codes are counted separately (shared, variable width).
+__host__ __device__ inline int conv_wave_words(int Gp, int nit, int NC2, int PWs, bool stg,
+                                               bool ext, bool vthn) {
+  const int vs = conv_vs(PWs, NC2);
+  int w = kWave * 4 + kWave * 2 + (stg ? kWave * nit * 2 : 0) + 2 * conv_tcn(PWs) + Gp +
+          Gp * vs * (1 + (ext ? 2 : 0) + (vthn ? 1 : 0));
+  return (w + 3) & ~3;
+}
+
+// LDS layout of a conv_layer_kernel work-group, in 4-byte words: a shared part (decay
+// table, ballot-bit map, reduction slots, int32 weight codes per channel group), then
+// one region per wave.
 struct ConvLds {
   int ext, lanemap, red, qs, shared_words;                        // shared
   int rec, rec1, stg, tc, vthc, v, mn, mx, th, wave_words;        // per wave
-  int vs, qst, tcn;  // slot strides (odd, with spare words), TC entries
+  int vs, qst, tcn;
   int words;
 };
 
@@ -85,9 +108,9 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int ncg, int nsb
                                                    int nit, int ICKK, int NC2, int PWs,
                                                    bool ext, bool vthn) {
   ConvLds l;
-  l.vs = (PWs + NC2) | 1;   // positions, then one spare word per candidate
-  l.qst = (ICKK + 1) | 1;   // codes, then at least one zero word
-  l.tcn = PWs + kWave;      // positions, then one spare entry per lane
+  l.vs = conv_vs(PWs, NC2);
+  l.qst = conv_qs(ICKK);
+  l.tcn = conv_tcn(PWs);
   int o = 0;
   l.ext = o;     o += n_table + 2;
   l.lanemap = o; o += 2 * kWave;  // int2 {slot, position offset} per ballot bit
@@ -111,14 +134,16 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int ncg, int nsb
   return l;
 }
 
-// Per-lane constants and LDS pointers of one wave (see the file comment).
+// Per-lane constants and LDS pointers of one wave (see the file comment).  CT: the
+// type the weight codes q*2^f_V are held in (int32, or narrower when they fit).
+template <typename CT>
 struct ConvLane {
   int4* rec;
   int2* rec1;
   uint64_t* stg;
   int2* tc;
-  int32_t* ext;
-  int32_t* qs;
+  const int32_t* ext;
+  const CT* qs;
   int32_t* Vs;
   int32_t* mn;
   int32_t* mx;
@@ -131,20 +156,101 @@ struct ConvLane {
   int cand, oc_lane, mql, ntab;
 };
 
+// Lane constants for a wave of Gi slots per iteration over a band of PWs positions
+// (slot strides VS / QS), whose first channel is oc0.
+template <typename CT>
+__device__ __forceinline__ void conv_lane_setup(ConvLane<CT>& c, const ConvGeom& g, int lane,
+                                                int Gi, int VS, int QS, int PWs, int oc0,
+                                                int ntab) {
+  const int slot0 = lane / g.NC2;
+  c.cand = lane - slot0 * g.NC2;
+  const int dy = c.cand / g.NC, dx = c.cand - (c.cand / g.NC) * g.NC;
+  const bool lane_on = slot0 < Gi;
+  const int slot_t = lane_on ? slot0 : 0;
+  c.lm = lane_on ? (1ull << c.cand) : 0ull;
+  c.first = (lane_on && slot0 == 0) ? 1 : 0;
+  c.lp = dy * g.W + dx;
+  c.lv = slot0 * VS + c.lp;
+  c.lq = slot0 * QS - dy * g.S * g.K - dx * g.S;
+  c.v_spare = slot_t * VS + PWs + c.cand;
+  c.q_zero = slot_t * QS + g.IC * g.K * g.K;
+  c.tc_spare = PWs + lane;
+  c.GiVS = Gi * VS;
+  c.GiQS = Gi * QS;
+  c.oc_lane = oc0 + slot0;
+  c.mql = g.mql;
+  c.ntab = ntab;
+}
+
+// Decodes the events of one chunk (connectivity/conv.py:15-43), one per lane (time tv,
+// source sv, index j; real when j < n_eff and sv >= 0), against the rows [r0, r0+rn):
+// records for the events with a candidate there, compacted in order.  Returns their
+// number; oy0/ox0 = the event's first candidate row and column.
+template <typename CT>
+__device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane<CT>& c, int tv,
+                                           int sv, int j, int n_eff, int r0, int rn, int& oy0,
+                                           int& ox0) {
+  const bool real = j < n_eff && sv >= 0;
+  int ch = 0, y = 0, x = 0;
+  if (real) {
+    ch = sv / g.HWin;
+    const int rem = sv - ch * g.HWin;
+    y = rem / g.Win;
+    x = rem - y * g.Win;
+    ch = min(ch, g.IC - 1);  // memory safety only; the host rejects such ids
+  }
+  // Candidate output rows [ceil((y+P-K+1)/S), floor((y+P)/S)] within [r0, r0+rn) and
+  // columns within [0, W) (connectivity/conv.py:15-29).
+  oy0 = floordiv_pos(y + g.P - g.K + g.S, g.S);
+  ox0 = floordiv_pos(x + g.P - g.K + g.S, g.S);
+  const int dyA = max(oy0, r0) - oy0, dyB = min((y + g.P) / g.S, r0 + rn - 1) - oy0;
+  const int dxA = max(ox0, 0) - ox0, dxB = min((x + g.P) / g.S, g.W - 1) - ox0;
+  const bool rel = real && dyA <= dyB && dxA <= dxB;
+  uint64_t m = 0;
+  if (rel) {
+    const uint64_t cols = (2ull << dxB) - (1ull << dxA);
+    for (int d = dyA; d <= dyB; ++d) m |= cols << (d * g.NC);
+  }
+  const int p0 = (oy0 - r0) * g.W + ox0;
+  const int q0 = ch * g.K * g.K + (y + g.P - oy0 * g.S) * g.K + (x + g.P - ox0 * g.S);
+  const uint64_t relm = __ballot(rel);
+  if (rel) {
+    const int slot = lanes_below(relm);
+    c.rec[slot] = make_int4(tv, p0, q0, (int)(uint32_t)m);
+    c.rec1[slot] = make_int2((int)(uint32_t)(m >> 32), j);
+  }
+  return __popcll(relm);
+}
+
+// Where a wave's spikes go.
+enum ConvMode { kStage = 0, kMask = 1, kEmit = 2 };
+
+struct ConvSink {
+  int b;            // stream
+  // kMask: spike bits in global memory
+  uint32_t* masks;
+  int L, OC, WPO, Gi;
+  // kEmit: the ordered stream
+  float* out_t;
+  int32_t* out_s;
+  int cap, HW;
+};
+
 // The events of one decoded chunk, in order (salt_core/quant/scan.py:22-52 per update).
-// MERGE: stage the spike ballots for the work-group's merge; otherwise set spike bits
-// in global memory.
-template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, bool MERGE>
-__device__ __forceinline__ void conv_events(const ConvArgs& a, const ConvLane& c,
-                                            const int (&vtc)[NIT], int n_ev, int base, int b,
-                                            int& vmin_l, int& vmax_l) {
+// kStage: stage the spike ballots for the work-group's merge; kMask: set spike bits in
+// global memory; kEmit: the wave holds the whole layer and appends its spikes to the
+// stream (out_n: spikes so far, wave-uniform).
+template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, int MODE, typename CT>
+__device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane<CT>& c,
+                                            const int (&vtc)[NIT], int n_ev, int base,
+                                            const ConvSink& sk, int& out_n, int& vmin_l,
+                                            int& vmax_l) {
   if (n_ev == 0) return;
-  // MERGE: lane e of sg_lo/sg_hi[it] collects event e's spike ballot; they are
+  // kStage: lane e of sg_lo/sg_hi[it] collects event e's spike ballot; they are
   // stored once per chunk.
   uint32_t sg_lo[NIT], sg_hi[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) { sg_lo[it] = 0; sg_hi[it] = 0; }
-  const Quant& qz = a.qz;
   const int fa = qz.fa, rc = qz.rc;
   const int lane = threadIdx.x & (kWave - 1);
   // Software pipeline: the record of event e+1 and its positions' (time, count) are
@@ -170,7 +276,7 @@ __device__ __forceinline__ void conv_events(const ConvArgs& a, const ConvLane& c
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       v[it] = c.Vs[va + it * c.GiVS];
-      qv[it] = c.qs[qa + it * c.GiQS];
+      qv[it] = (int)c.qs[qa + it * c.GiQS];
       vt[it] = VTHN ? c.th[va + it * c.GiVS] : vtc[it];
       if (EXT) { mnv[it] = c.mn[va + it * c.GiVS]; mxv[it] = c.mx[va + it * c.GiVS]; }
     }
@@ -195,15 +301,25 @@ __device__ __forceinline__ void conv_events(const ConvArgs& a, const ConvLane& c
     const bool mine = lane == e;
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-      if (MERGE) {
+      if (MODE == kStage) {
         sg_lo[it] = mine ? (uint32_t)bal[it] : sg_lo[it];
         sg_hi[it] = mine ? (uint32_t)(bal[it] >> 32) : sg_hi[it];
       } else if (bal[it]) {
-        if ((bal[it] >> lane) & 1) {
+        const bool fired = (bal[it] >> lane) & 1;
+        if (MODE == kEmit) {
+          // Lane order = (channel slot, row, column) = ascending neuron id, and the
+          // iterations ascend in channel: the order of salt_core/stream.py:24-46.
+          const int idx = out_n + lanes_below(bal[it]);
+          if (fired && idx < sk.cap) {
+            sk.out_t[(size_t)sk.b * sk.cap + idx] = (float)r.x;
+            sk.out_s[(size_t)sk.b * sk.cap + idx] = (c.oc_lane + it * sk.Gi) * sk.HW + pa;
+          }
+          out_n += __popcll(bal[it]);
+        } else if (fired) {
           // Bit = candidate index in the event's NC x NC grid (compaction decodes it).
-          const size_t w = ((size_t)b * a.L + r1.y) * (size_t)(a.OC * a.WPO) +
-                           (size_t)(c.oc_lane + it * a.Gi) * a.WPO + (c.cand >> 5);
-          atomicOr(&a.masks[w], 1u << (c.cand & 31));
+          const size_t w = ((size_t)sk.b * sk.L + r1.y) * (size_t)(sk.OC * sk.WPO) +
+                           (size_t)(c.oc_lane + it * sk.Gi) * sk.WPO + (c.cand >> 5);
+          atomicOr(&sk.masks[w], 1u << (c.cand & 31));
         }
       }
     }
@@ -213,7 +329,7 @@ __device__ __forceinline__ void conv_events(const ConvArgs& a, const ConvLane& c
     st = stn;
     asm volatile("" ::: "memory");  // keep this event's LDS traffic before the next one's
   }
-  if (MERGE && lane < n_ev) {
+  if (MODE == kStage && lane < n_ev) {
     const int jc = c.rec1[lane].y - base;  // the event's index within the chunk
 #pragma unroll
     for (int it = 0; it < NIT; ++it)
@@ -221,9 +337,46 @@ __device__ __forceinline__ void conv_events(const ConvArgs& a, const ConvLane& c
   }
 }
 
+// Catch-up column: decay to the last real input time T (connectivity/conv.py:102-125),
+// then the final registers of this wave's ocn channels over its PW positions.  An empty
+// position's catch-up has dt = 0; the identity columns after it repeat V.  A full queue
+// has no catch-up column.  Returns the largest per-position event count.
+template <bool F24, bool EXT, typename CT>
+__device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane<CT>& c, int lane,
+                                           int T, int ocn, int PW, int VS, size_t v_base,
+                                           int HW, int32_t* v_final, int32_t* v_min,
+                                           int32_t* v_max, int& vmin_l, int& vmax_l) {
+  int maxcnt = 0;
+  for (int i = lane; i < PW; i += kWave) maxcnt = max(maxcnt, c.tc[i].y);
+  for (int li = lane; li < ocn * PW; li += kWave) {
+    const int s = li / PW;
+    const int p = li - s * PW;
+    const int2 st = c.tc[p];
+    const int vi = s * VS + p;
+    int32_t vv = c.Vs[vi];
+    int32_t mnn = EXT ? c.mn[vi] : 0, mxx = EXT ? c.mx[vi] : 0;
+    if (st.y < c.mql) {
+      const int dt = st.y > 0 ? T - st.x : 0;
+      vv = decay_mul<F24>(vv, c.ext[decay_slot(dt, c.ntab)], qz.fa, qz.rc);  // |D| <= |V|
+      vmin_l = min(vmin_l, vv);
+      vmax_l = max(vmax_l, vv);
+      mnn = min(mnn, vv);
+      mxx = max(mxx, vv);
+    }
+    const size_t ng = v_base + (size_t)s * HW + p;
+    if (v_final) v_final[ng] = vv;
+    if (EXT) {
+      v_min[ng] = mnn;
+      v_max[ng] = mxx;
+    }
+  }
+  return wave_max(maxcnt);
+}
+
 template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN>
 __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvArgs a) {
   extern __shared__ int32_t smem[];
+  const ConvGeom& g = a.g;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -232,21 +385,22 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   const int cg = wv % a.ncg, sb = wv / a.ncg;  // channel group, sub-band
   const int Gi = a.Gi, Gp = NIT * a.Gi;
   const int oc0 = cg * a.G;
-  const int ocn = max(0, min(a.G, a.OC - oc0));
-  const int rows_end = min(a.H, (int)blockIdx.x * a.R + a.R);
+  const int ocn = max(0, min(a.G, g.OC - oc0));
+  const int rows_end = min(g.H, (int)blockIdx.x * a.R + a.R);
   const int r0 = blockIdx.x * a.R + sb * a.Rw;
   const int rn = max(0, min(a.Rw, rows_end - r0));
-  const int W = a.W, PWs = a.Rw * W, PW = rn * W;
-  const int KK = a.K * a.K, ICKK = a.IC * KK;
+  const int W = g.W, PWs = a.Rw * W, PW = rn * W;
+  const int ICKK = g.IC * g.K * g.K;
   const Quant& qz = a.qz;
-  const ConvLds lay = conv_lds_layout(qz.n_table, a.ncg, a.nsb, Gp, NIT, ICKK, a.NC2, PWs,
+  const ConvLds lay = conv_lds_layout(qz.n_table, a.ncg, a.nsb, Gp, NIT, ICKK, g.NC2, PWs,
                                       EXT, VTHN);
   const int VS = lay.vs, QS = lay.qst;
   int32_t* wbase = smem + lay.shared_words + wv * lay.wave_words;
   int2* lanemap = reinterpret_cast<int2*>(smem + lay.lanemap);
   int32_t* red = smem + lay.red;
-  ConvLane c;
-  c.ext = smem + lay.ext;
+  int32_t* ext = smem + lay.ext;
+  ConvLane<int32_t> c;
+  c.ext = ext;
   c.qs = smem + lay.qs + cg * Gp * QS;
   c.rec = reinterpret_cast<int4*>(wbase + lay.rec);
   c.rec1 = reinterpret_cast<int2*>(wbase + lay.rec1);
@@ -259,17 +413,17 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   c.th = wbase + lay.th;
 
   // ---- shared state: decay table, ballot bit -> (slot, position offset), codes
-  load_ext_table(c.ext, a.table, qz.n_table, qz.fa, tid, nthr);
+  load_ext_table(ext, a.table, qz.n_table, qz.fa, tid, nthr);
   for (int k = tid; k < kWave; k += nthr) {
-    const int s = k / a.NC2, cd = k - s * a.NC2;
-    lanemap[k] = make_int2(s, (cd / a.NC) * W + (cd - (cd / a.NC) * a.NC));
+    const int s = k / g.NC2, cd = k - s * g.NC2;
+    lanemap[k] = make_int2(s, (cd / g.NC) * W + (cd - (cd / g.NC) * g.NC));
   }
   for (int i = tid; i < a.ncg * Gp * QS; i += nthr) {
-    const int g = i / (Gp * QS), rem = i - g * (Gp * QS);
+    const int gi = i / (Gp * QS), rem = i - gi * (Gp * QS);
     const int s = rem / QS, k = rem - s * QS;
-    const int oc = g * a.G + s;
+    const int oc = gi * a.G + s;
     // Codes are stored pre-shifted, q * 2^f_V in two's complement (U = D + q*2^f_V).
-    smem[lay.qs + i] = (s < a.G && oc < a.OC && k < ICKK)
+    smem[lay.qs + i] = (s < a.G && oc < g.OC && k < ICKK)
                            ? (int32_t)((uint32_t)load_code_bits(a.q, (size_t)oc * ICKK + k,
                                                                 a.q_bits) << qz.fV)
                            : 0;
@@ -288,34 +442,19 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
     if (EXT) { c.mn[i] = 0; c.mx[i] = 0; }
     if (VTHN) {
       const int s = i / VS, p = i - s * VS;
-      c.th[i] = (s < ocn && p < PW) ? qz.vth[(size_t)(oc0 + s) * a.HW + r0 * W + p] : INT_MAX;
+      c.th[i] = (s < ocn && p < PW) ? qz.vth[(size_t)(oc0 + s) * g.HW + r0 * W + p] : INT_MAX;
     }
   }
   for (int i = lane; i < lay.tcn; i += kWave) c.tc[i] = make_int2(0, 0);
   __syncthreads();
 
-  // ---- lane constants
-  const int slot0 = lane / a.NC2;
-  c.cand = lane - slot0 * a.NC2;
-  const int dy = c.cand / a.NC, dx = c.cand - (c.cand / a.NC) * a.NC;
-  const bool lane_on = slot0 < Gi;
-  const int slot_t = lane_on ? slot0 : 0;
-  c.lm = lane_on ? (1ull << c.cand) : 0ull;
-  c.first = (lane_on && slot0 == 0) ? 1 : 0;
-  c.lp = dy * W + dx;
-  c.lv = slot0 * VS + c.lp;
-  c.lq = slot0 * QS - dy * a.S * a.K - dx * a.S;
-  c.v_spare = slot_t * VS + PWs + c.cand;
-  c.q_zero = slot_t * QS + ICKK;
-  c.tc_spare = PWs + lane;
-  c.GiVS = Gi * VS;
-  c.GiQS = Gi * QS;
-  c.oc_lane = oc0 + slot0;
-  c.mql = a.mql;
-  c.ntab = qz.n_table;
+  conv_lane_setup(c, g, lane, Gi, VS, QS, PWs, oc0, qz.n_table);
   int vtc[NIT];
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) vtc[it] = vthc[min(it * Gi + slot0, Gp - 1)];
+  for (int it = 0; it < NIT; ++it) vtc[it] = vthc[min(it * Gi + c.oc_lane - oc0, Gp - 1)];
+  ConvSink sk;
+  sk.b = b; sk.masks = a.masks; sk.L = a.L; sk.OC = g.OC; sk.WPO = a.WPO; sk.Gi = Gi;
+  sk.out_t = a.out_t; sk.out_s = a.out_s; sk.cap = a.cap; sk.HW = g.HW;
 
   const int L = a.L;
   const int nr = a.n_real[b];
@@ -331,7 +470,6 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   if (lane < n_eff) { t_n = time_ms(tb[lane]); s_n = sb_src[lane]; }
 
   for (int base = 0; base < n_eff; base += kWave) {
-    // ---- decode 64 events (connectivity/conv.py:15-43), one per lane
     const int j = base + lane;
     const int tv = t_n, sv = s_n;
     {
@@ -339,51 +477,24 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
       t_n = 0; s_n = -1;
       if (j2 < n_eff) { t_n = time_ms(tb[j2]); s_n = sb_src[j2]; }
     }
-    const bool real = j < n_eff && sv >= 0;
-    int ch = 0, y = 0, x = 0;
-    if (real) {
-      ch = sv / a.HWin;
-      const int rem = sv - ch * a.HWin;
-      y = rem / a.Win;
-      x = rem - y * a.Win;
-      ch = min(ch, a.IC - 1);  // memory safety only; the host rejects such ids
-    }
-    // Candidate output rows [ceil((y+P-K+1)/S), floor((y+P)/S)] within [r0, r0+rn) and
-    // columns within [0, W) (connectivity/conv.py:15-29).
-    const int oy0 = floordiv_pos(y + a.P - a.K + a.S, a.S);
-    const int ox0 = floordiv_pos(x + a.P - a.K + a.S, a.S);
-    const int dyA = max(oy0, r0) - oy0, dyB = min((y + a.P) / a.S, r0 + rn - 1) - oy0;
-    const int dxA = max(ox0, 0) - ox0, dxB = min((x + a.P) / a.S, W - 1) - ox0;
-    const bool rel = real && dyA <= dyB && dxA <= dxB;
-    uint64_t m = 0;
-    if (rel) {
-      const uint64_t cols = (2ull << dxB) - (1ull << dxA);
-      for (int d = dyA; d <= dyB; ++d) m |= cols << (d * a.NC);
-    }
-    const int p0 = (oy0 - r0) * W + ox0;
-    const int q0 = ch * KK + (y + a.P - oy0 * a.S) * a.K + (x + a.P - ox0 * a.S);
-    const uint64_t relm = __ballot(rel);
-    const int n_ev = __popcll(relm);
-    if (rel) {
-      const int slot = lanes_below(relm);
-      c.rec[slot] = make_int4(tv, p0, q0, (int)(uint32_t)m);
-      c.rec1[slot] = make_int2((int)(uint32_t)(m >> 32), j);
-    }
+    int oy0, ox0;
+    const int n_ev = conv_decode(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0);
     if (a.merge)
       for (int i = lane; i < kWave * NIT; i += kWave) c.stg[i] = 0;
     __syncthreads();
     if (a.merge) {
-      conv_events<NIT, F24, SAT, EXT, VTHN, true>(a, c, vtc, n_ev, base, b, vmin_l, vmax_l);
+      conv_events<NIT, F24, SAT, EXT, VTHN, kStage>(qz, c, vtc, n_ev, base, sk, out_base,
+                                                     vmin_l, vmax_l);
       __syncthreads();  // every wave's ballots of this chunk are staged
       if (wv == 0) {
         // Walk (event, channel group, iteration, bit) = (event, ascending neuron id);
         // the sub-bands' ballots of one event are disjoint and share the lane mapping.
         const int nw = a.ncg * a.nsb;
         int cnt = 0;
-        for (int g = 0; g < a.ncg; ++g)
+        for (int gi = 0; gi < a.ncg; ++gi)
           for (int it = 0; it < NIT; ++it) {
             uint64_t bits = 0;
-            for (int w = g; w < nw; w += a.ncg)
+            for (int w = gi; w < nw; w += a.ncg)
               bits |= reinterpret_cast<const uint64_t*>(
                   smem + lay.shared_words + w * lay.wave_words + lay.stg)[lane * NIT + it];
             cnt += __popcll(bits);
@@ -394,20 +505,20 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
           const float te = (float)tv;
           const int pg = oy0 * W + ox0;  // plane position of the event's first candidate
           int pos = out_base + excl;
-          for (int g = 0; g < a.ncg; ++g)
+          for (int gi = 0; gi < a.ncg; ++gi)
             for (int it = 0; it < NIT; ++it) {
               uint64_t bits = 0;
-              for (int w = g; w < nw; w += a.ncg)
+              for (int w = gi; w < nw; w += a.ncg)
                 bits |= reinterpret_cast<const uint64_t*>(
                     smem + lay.shared_words + w * lay.wave_words + lay.stg)[lane * NIT + it];
               while (bits) {
                 const int k = __builtin_ctzll(bits);
                 bits &= bits - 1;
                 const int2 lmk = lanemap[k];
-                const int oc = g * a.G + it * Gi + lmk.x;
+                const int oc = gi * a.G + it * Gi + lmk.x;
                 if (pos < a.cap) {
                   a.out_t[(size_t)b * a.cap + pos] = te;
-                  a.out_s[(size_t)b * a.cap + pos] = oc * a.HW + pg + lmk.y;
+                  a.out_s[(size_t)b * a.cap + pos] = oc * g.HW + pg + lmk.y;
                 }
                 ++pos;
               }
@@ -417,42 +528,18 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
       }
       __syncthreads();  // the staging and records are rewritten by the next chunk
     } else {
-      conv_events<NIT, F24, SAT, EXT, VTHN, false>(a, c, vtc, n_ev, base, b, vmin_l, vmax_l);
+      conv_events<NIT, F24, SAT, EXT, VTHN, kMask>(qz, c, vtc, n_ev, base, sk, out_base,
+                                                    vmin_l, vmax_l);
       __syncthreads();  // records are rewritten by the next chunk
     }
   }
 
-  // ---- catch-up column: decay to the last real input time T
-  // (connectivity/conv.py:102-125).  An empty position's catch-up has dt = 0; the
-  // identity columns after it repeat V.  A full queue has no catch-up column.
   const int T = n_eff > 0 ? time_ms(tb[n_eff - 1]) : 0;
-  int maxcnt = 0;
-  for (int i = lane; i < PW; i += kWave) maxcnt = max(maxcnt, c.tc[i].y);
-  for (int li = lane; li < ocn * PW; li += kWave) {
-    const int s = li / PW;
-    const int p = li - s * PW;
-    const int2 st = c.tc[p];
-    const int vi = s * VS + p;
-    int32_t vv = c.Vs[vi];
-    int32_t mnn = EXT ? c.mn[vi] : 0, mxx = EXT ? c.mx[vi] : 0;
-    if (st.y < a.mql) {
-      const int dt = st.y > 0 ? T - st.x : 0;
-      vv = decay_mul<F24>(vv, c.ext[decay_slot(dt, c.ntab)], qz.fa, qz.rc);  // |D| <= |V|
-      vmin_l = min(vmin_l, vv);
-      vmax_l = max(vmax_l, vv);
-      mnn = min(mnn, vv);
-      mxx = max(mxx, vv);
-    }
-    const size_t ng = (size_t)b * (a.OC * a.HW) + (size_t)(oc0 + s) * a.HW + r0 * W + p;
-    if (a.v_final) a.v_final[ng] = vv;
-    if (EXT) {
-      a.v_min[ng] = mnn;
-      a.v_max[ng] = mxx;
-    }
-  }
+  int maxcnt = conv_finish<F24, EXT>(qz, c, lane, T, ocn, PW, VS,
+                                     (size_t)b * (g.OC * g.HW) + (size_t)oc0 * g.HW + r0 * W,
+                                     g.HW, a.v_final, a.v_min, a.v_max, vmin_l, vmax_l);
   vmin_l = wave_min(vmin_l);
   vmax_l = wave_max(vmax_l);
-  maxcnt = wave_max(maxcnt);
   if (lane == 0) {
     red[wv * 4 + 0] = vmin_l;
     red[wv * 4 + 1] = vmax_l;

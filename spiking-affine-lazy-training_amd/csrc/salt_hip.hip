@@ -340,6 +340,14 @@ Quant make_quant(const salt_qparams* p) {
   return q;
 }
 
+ConvGeom conv_geom(const salt_layer_desc* d, const ConvPlan& pl) {
+  ConvGeom g;
+  g.IC = d->ic; g.Win = d->w_in; g.HWin = d->h_in * d->w_in; g.OC = d->oc;
+  g.K = d->k; g.S = d->s; g.P = d->p; g.H = pl.H; g.W = pl.W; g.HW = pl.HW;
+  g.NC = pl.NC; g.NC2 = pl.NC2; g.mql = d->max_queue_len;
+  return g;
+}
+
 size_t mask_bytes_conv(const ConvPlan& pl, const salt_layer_desc* d, int B, int L) {
   return pl.merge ? 0 : (size_t)B * L * d->oc * pl.WPO * 4;
 }
@@ -482,10 +490,8 @@ int32_t salt_layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     if (workspace_bytes < need || (need && !d_workspace))
       return fail(-1, "workspace of %zu bytes below the %zu needed", workspace_bytes, need);
     ConvArgs a;
-    a.IC = desc->ic; a.Win = desc->w_in; a.HWin = desc->h_in * desc->w_in;
-    a.OC = desc->oc; a.K = desc->k; a.S = desc->s; a.P = desc->p;
-    a.H = pl.H; a.W = pl.W; a.HW = pl.HW; a.NC = pl.NC; a.NC2 = pl.NC2; a.WPO = pl.WPO;
-    a.mql = desc->max_queue_len;
+    a.g = conv_geom(desc, pl);
+    a.WPO = pl.WPO;
     a.G = pl.G; a.Gi = pl.Gi; a.ncg = pl.ncg; a.nsb = pl.nsb; a.Rw = pl.Rw; a.R = pl.R;
     a.qz = qz; a.table = prm->d_decay_table; a.q = prm->d_q; a.q_bits = prm->q_bits;
     a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
@@ -504,7 +510,7 @@ int32_t salt_layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     if (!pl.merge) {
       CompactArgs c;
       c.conv = 1; c.words = desc->oc * pl.WPO; c.WPO = pl.WPO; c.NC = pl.NC; c.OC = desc->oc;
-      c.HW = pl.HW; c.W = pl.W; c.HWin = a.HWin; c.Win = desc->w_in; c.K = desc->k;
+      c.HW = pl.HW; c.W = pl.W; c.HWin = a.g.HWin; c.Win = desc->w_in; c.K = desc->k;
       c.S = desc->s; c.P = desc->p; c.L = L; c.times = in->d_times; c.src = in->d_src;
       c.n_real = in->d_n_real; c.masks = a.masks; c.cap = out->cap;
       c.fill_pads = out->fill_pads; c.out_t = out->d_times; c.out_s = out->d_src;
