@@ -117,28 +117,19 @@ def main() -> int:
     torch.cuda.synchronize()
     fits = runner.check_fits(outs)
 
-    # Timed region: K steps bracketed by synchronize; per-layer HIP events on the stream
-    # the kernels are launched on (torch's current stream).
+    # Timed region: K steps bracketed by synchronize, each one salt_layer_forward per
+    # layer (the calls salt_network_forward makes), with HIP events around each layer's
+    # launch on the stream the kernels run on (torch's current stream).
     ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(n_layers)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    from salt_amd.quant.backend import run_layer_kernel
     for k in range(args.steps):
-        times, src, n_real = stream.event_times, stream.event_source_idx, stream.n_real_events
-        outs = []
-        for i, (layer, dp) in enumerate(zip(net.layers, runner.dev_params)):
-            ev[k][i][0].record()
-            o = run_layer_kernel(layer, dp, runner.round_mode, times, src, n_real,
-                                 int(layer.max_out_spikes), extremes=False,
-                                 fill_pads=(i == n_layers - 1))
-            ev[k][i][1].record()
-            outs.append(o)
-            times, src, n_real = o.times, o.src, o.n
+        outs = runner.run_layers(stream, around=lambda i, ph, k=k: ev[k][i][ph].record())
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    layer_ms = np.array([[ev[k][i][0].elapsed_time(ev[k][i][1]) for i in range(n_layers)]
-                         for k in range(args.steps)]).mean(axis=0)
+    launch_ms = np.array([[ev[k][i][0].elapsed_time(ev[k][i][1]) for i in range(n_layers)]
+                          for k in range(args.steps)]).mean(axis=0)
     ms_per_step = wall * 1000.0 / args.steps
     value = n_events / (ms_per_step / 1000.0)
 
@@ -157,16 +148,16 @@ def main() -> int:
         spikes = int(host[i][1].sum())
         lds = updates * (8 + wbytes)
         hbm = 8 * n_in_events + 8 * spikes + 4 * B * layer.n_neurons + dp.q.numel() * wbytes
-        per_layer.append(dict(name=layer.name, ms=float(layer_ms[i]), updates=updates,
-                              spikes=spikes, lds_bytes=lds, hbm_bytes=hbm))
+        per_layer.append(dict(name=layer.name, updates=updates, spikes=spikes, lds_bytes=lds,
+                              hbm_bytes=hbm, ms=float(launch_ms[i])))
         in_src, in_n = host[i]
-    # Dominant kernel = the slowest layer.  Memory roof: HBM (the path does no MFMA
-    # work); the LDS figure beside it is the on-chip roof the per-update traffic meets.
+    # Dominant kernel: the slowest layer.  Memory roof: HBM (the path does no MFMA work);
+    # the LDS figure beside it is the on-chip roof the per-update traffic meets.
     dom = max(per_layer, key=lambda d: d["ms"])
     lds_gbs = dom["lds_bytes"] / (dom["ms"] * 1e-3) / 1e9
     hbm_gbs = dom["hbm_bytes"] / (dom["ms"] * 1e-3) / 1e9
     lds_frac, hbm_frac = lds_gbs / LDS_PEAK_GBS, hbm_gbs / HBM_PEAK_GBS
-    roofline = {"bound": "hbm", "kernel": dom["name"],
+    roofline = {"bound": "hbm", "kernel": dom["name"], "launch_ms": round(dom["ms"], 4),
                 "achieved": round(hbm_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(hbm_frac, 6), "traffic": measured_traffic(dom["name"]),
                 "algorithmic_bytes": dom["hbm_bytes"],
@@ -219,7 +210,8 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int32",
         "data": "synthetic",
         "config": {"workload": w.name, "streams": B, "padded_len": L, "input_events": n_events,
-                   "layers": [l.name for l in net.layers], "round_mode": w.round_mode,
+                   "layers": [l.name for l in net.layers],
+                   "round_mode": w.round_mode,
                    "f_a": 10, "f_V": 0, "i_V": 24, "overflow": "wrap"},
         "bit_exact": bit_exact, "fits": bool(fits.all()),
         "roofline": roofline, "cpu_baseline": cpu,

@@ -147,6 +147,29 @@ int32_t salt_layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
                            const salt_layer_result* result, void* d_workspace,
                            size_t workspace_bytes, void* stream);
 
+/* Bytes of device workspace salt_network_forward needs: the largest of the layers'
+ * salt_layer_workspace_size() (the layers run one after the other on one stream, so they
+ * share it), layer i > 0 reading a stream of L = descs[i-1].max_out_spikes entries. */
+int32_t salt_network_workspace_size(int32_t n_layers, const salt_layer_desc* descs,
+                                    const salt_qparams* prms, int32_t B, int32_t L,
+                                    int32_t want_neuron_extremes, size_t* bytes);
+
+/*
+ * A whole network over a batch in one call: replaces run_network's layer loop
+ * (salt_core/network.py:93-122, each layer's output stream feeding the next).  Layer i
+ * runs as salt_layer_forward with input outs[i-1] (L = its cap, n_real = its d_n, of
+ * which the first min(d_n, cap) entries are read), all on `stream` with no host
+ * synchronisation.  descs/prms/outs/results: arrays of n_layers entries, as for
+ * salt_layer_forward; every results[i] gives both or neither of d_v_min/d_v_max.  All
+ * arguments are checked before the first launch.  A stream whose layer i exceeded its
+ * cap feeds layer i+1 with the first cap spikes in (event, neuron) order (fits = false:
+ * the reference's truncation keeps a different subset, salt_core/stream.py:60).
+ */
+int32_t salt_network_forward(int32_t n_layers, const salt_layer_desc* descs,
+                             const salt_qparams* prms, const salt_events_in* in,
+                             const salt_events_out* outs, const salt_layer_result* results,
+                             void* d_workspace, size_t workspace_bytes, void* stream);
+
 /* Order-sensitive 64-bit hash per stream, for streams too large to copy back.
  * With mix64 = the splitmix64 finaliser (add 0x9E3779B97F4A7C15, then xor-shift-multiply
  * by 0xBF58476D1CE4E5B9 and 0x94D049BB133111EB), entry i < min(n, cap) contributes

@@ -32,8 +32,7 @@
 // channel group, iteration, lane) = (event, ascending neuron id) -- the order of
 // salt_core/stream.py:24-46 -- appending to the stream.  With several work-groups per
 // stream (state above the LDS size) each wave sets per-event spike bits in global
-// memory instead, and a compaction kernel orders them.  A wave that holds a whole
-// layer (the fused network kernel) appends its spikes to the stream itself.
+// memory instead, and a compaction kernel orders them.
 //
 // No barrier inside the event loop: a wave's LDS operations complete in program
 // order, so event e+1 reads what event e wrote.
@@ -134,16 +133,14 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int ncg, int nsb
   return l;
 }
 
-// Per-lane constants and LDS pointers of one wave (see the file comment).  CT: the
-// type the weight codes q*2^f_V are held in (int32, or narrower when they fit).
-template <typename CT>
+// Per-lane constants and LDS pointers of one wave (see the file comment).
 struct ConvLane {
   int4* rec;
   int2* rec1;
   uint64_t* stg;
   int2* tc;
   const int32_t* ext;
-  const CT* qs;
+  const int32_t* qs;     // weight codes q*2^f_V
   int32_t* Vs;
   int32_t* mn;
   int32_t* mx;
@@ -158,8 +155,7 @@ struct ConvLane {
 
 // Lane constants for a wave of Gi slots per iteration over a band of PWs positions
 // (slot strides VS / QS), whose first channel is oc0.
-template <typename CT>
-__device__ __forceinline__ void conv_lane_setup(ConvLane<CT>& c, const ConvGeom& g, int lane,
+__device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, int lane,
                                                 int Gi, int VS, int QS, int PWs, int oc0,
                                                 int ntab) {
   const int slot0 = lane / g.NC2;
@@ -186,8 +182,7 @@ __device__ __forceinline__ void conv_lane_setup(ConvLane<CT>& c, const ConvGeom&
 // source sv, index j; real when j < n_eff and sv >= 0), against the rows [r0, r0+rn):
 // records for the events with a candidate there, compacted in order.  Returns their
 // number; oy0/ox0 = the event's first candidate row and column.
-template <typename CT>
-__device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane<CT>& c, int tv,
+__device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c, int tv,
                                            int sv, int j, int n_eff, int r0, int rn, int& oy0,
                                            int& ox0) {
   const bool real = j < n_eff && sv >= 0;
@@ -223,28 +218,22 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane<CT>
 }
 
 // Where a wave's spikes go.
-enum ConvMode { kStage = 0, kMask = 1, kEmit = 2 };
+enum ConvMode { kStage = 0, kMask = 1 };
 
+// kMask: the spike-bit words in global memory of stream b.
 struct ConvSink {
-  int b;            // stream
-  // kMask: spike bits in global memory
+  int b;
   uint32_t* masks;
   int L, OC, WPO, Gi;
-  // kEmit: the ordered stream
-  float* out_t;
-  int32_t* out_s;
-  int cap, HW;
 };
 
 // The events of one decoded chunk, in order (salt_core/quant/scan.py:22-52 per update).
 // kStage: stage the spike ballots for the work-group's merge; kMask: set spike bits in
-// global memory; kEmit: the wave holds the whole layer and appends its spikes to the
-// stream (out_n: spikes so far, wave-uniform).
-template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, int MODE, typename CT>
-__device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane<CT>& c,
+// global memory.
+template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, int MODE>
+__device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
                                             const int (&vtc)[NIT], int n_ev, int base,
-                                            const ConvSink& sk, int& out_n, int& vmin_l,
-                                            int& vmax_l) {
+                                            const ConvSink& sk, int& vmin_l, int& vmax_l) {
   if (n_ev == 0) return;
   // kStage: lane e of sg_lo/sg_hi[it] collects event e's spike ballot; they are
   // stored once per chunk.
@@ -276,7 +265,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane<CT>&
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       v[it] = c.Vs[va + it * c.GiVS];
-      qv[it] = (int)c.qs[qa + it * c.GiQS];
+      qv[it] = c.qs[qa + it * c.GiQS];
       vt[it] = VTHN ? c.th[va + it * c.GiVS] : vtc[it];
       if (EXT) { mnv[it] = c.mn[va + it * c.GiVS]; mxv[it] = c.mx[va + it * c.GiVS]; }
     }
@@ -304,23 +293,11 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane<CT>&
       if (MODE == kStage) {
         sg_lo[it] = mine ? (uint32_t)bal[it] : sg_lo[it];
         sg_hi[it] = mine ? (uint32_t)(bal[it] >> 32) : sg_hi[it];
-      } else if (bal[it]) {
-        const bool fired = (bal[it] >> lane) & 1;
-        if (MODE == kEmit) {
-          // Lane order = (channel slot, row, column) = ascending neuron id, and the
-          // iterations ascend in channel: the order of salt_core/stream.py:24-46.
-          const int idx = out_n + lanes_below(bal[it]);
-          if (fired && idx < sk.cap) {
-            sk.out_t[(size_t)sk.b * sk.cap + idx] = (float)r.x;
-            sk.out_s[(size_t)sk.b * sk.cap + idx] = (c.oc_lane + it * sk.Gi) * sk.HW + pa;
-          }
-          out_n += __popcll(bal[it]);
-        } else if (fired) {
-          // Bit = candidate index in the event's NC x NC grid (compaction decodes it).
-          const size_t w = ((size_t)sk.b * sk.L + r1.y) * (size_t)(sk.OC * sk.WPO) +
-                           (size_t)(c.oc_lane + it * sk.Gi) * sk.WPO + (c.cand >> 5);
-          atomicOr(&sk.masks[w], 1u << (c.cand & 31));
-        }
+      } else if ((bal[it] >> lane) & 1) {
+        // Bit = candidate index in the event's NC x NC grid (compaction decodes it).
+        const size_t w = ((size_t)sk.b * sk.L + r1.y) * (size_t)(sk.OC * sk.WPO) +
+                         (size_t)(c.oc_lane + it * sk.Gi) * sk.WPO + (c.cand >> 5);
+        atomicOr(&sk.masks[w], 1u << (c.cand & 31));
       }
     }
     r = rn;
@@ -341,8 +318,8 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane<CT>&
 // then the final registers of this wave's ocn channels over its PW positions.  An empty
 // position's catch-up has dt = 0; the identity columns after it repeat V.  A full queue
 // has no catch-up column.  Returns the largest per-position event count.
-template <bool F24, bool EXT, typename CT>
-__device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane<CT>& c, int lane,
+template <bool F24, bool EXT>
+__device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane& c, int lane,
                                            int T, int ocn, int PW, int VS, size_t v_base,
                                            int HW, int32_t* v_final, int32_t* v_min,
                                            int32_t* v_max, int& vmin_l, int& vmax_l) {
@@ -399,7 +376,7 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   int2* lanemap = reinterpret_cast<int2*>(smem + lay.lanemap);
   int32_t* red = smem + lay.red;
   int32_t* ext = smem + lay.ext;
-  ConvLane<int32_t> c;
+  ConvLane c;
   c.ext = ext;
   c.qs = smem + lay.qs + cg * Gp * QS;
   c.rec = reinterpret_cast<int4*>(wbase + lay.rec);
@@ -454,7 +431,6 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   for (int it = 0; it < NIT; ++it) vtc[it] = vthc[min(it * Gi + c.oc_lane - oc0, Gp - 1)];
   ConvSink sk;
   sk.b = b; sk.masks = a.masks; sk.L = a.L; sk.OC = g.OC; sk.WPO = a.WPO; sk.Gi = Gi;
-  sk.out_t = a.out_t; sk.out_s = a.out_s; sk.cap = a.cap; sk.HW = g.HW;
 
   const int L = a.L;
   const int nr = a.n_real[b];
@@ -483,8 +459,8 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
       for (int i = lane; i < kWave * NIT; i += kWave) c.stg[i] = 0;
     __syncthreads();
     if (a.merge) {
-      conv_events<NIT, F24, SAT, EXT, VTHN, kStage>(qz, c, vtc, n_ev, base, sk, out_base,
-                                                     vmin_l, vmax_l);
+      conv_events<NIT, F24, SAT, EXT, VTHN, kStage>(qz, c, vtc, n_ev, base, sk, vmin_l,
+                                                     vmax_l);
       __syncthreads();  // every wave's ballots of this chunk are staged
       if (wv == 0) {
         // Walk (event, channel group, iteration, bit) = (event, ascending neuron id);
@@ -528,8 +504,8 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
       }
       __syncthreads();  // the staging and records are rewritten by the next chunk
     } else {
-      conv_events<NIT, F24, SAT, EXT, VTHN, kMask>(qz, c, vtc, n_ev, base, sk, out_base,
-                                                    vmin_l, vmax_l);
+      conv_events<NIT, F24, SAT, EXT, VTHN, kMask>(qz, c, vtc, n_ev, base, sk, vmin_l,
+                                                    vmax_l);
       __syncthreads();  // records are rewritten by the next chunk
     }
   }

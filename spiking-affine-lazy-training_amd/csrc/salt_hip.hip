@@ -377,6 +377,114 @@ hipError_t launch_conv(const ConvArgs& a, const ConvPlan& pl, int flags, int B,
 
 constexpr size_t kFcWeightLds = 40 * 1024;  // stage FC weight slices up to this size
 
+// Checks the arguments of one layer call (launch = 0) or, once they are known to be
+// valid, enqueues it on st (launch = 1).
+int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
+                      const salt_events_in* in, const salt_events_out* out,
+                      const salt_layer_result* res, void* d_workspace, size_t workspace_bytes,
+                      hipStream_t st, int launch) {
+  int32_t rc = check_common(desc, prm);
+  if (rc) return rc;
+  if (!in || !out || !res) return fail(-1, "null events or result descriptor");
+  const int B = in->B, L = in->L;
+  if (B < 0 || L < 0) return fail(-1, "invalid batch shape B=%d L=%d", B, L);
+  if (B > 65535) return fail(-1, "batch of %d streams above 65535", B);
+  if (B == 0) return 0;
+  if (!in->d_n_real || (L > 0 && (!in->d_times || !in->d_src)))
+    return fail(-1, "input events missing");
+  if (out->cap != desc->max_out_spikes) return fail(-1, "out.cap must equal max_out_spikes");
+  if (!out->d_n || (out->cap > 0 && (!out->d_times || !out->d_src)))
+    return fail(-1, "output stream buffers missing");
+  if (!res->d_stats) return fail(-1, "stats buffer missing");
+  if ((res->d_v_min == nullptr) != (res->d_v_max == nullptr))
+    return fail(-1, "give both or neither of v_min/v_max");
+  const bool ext = res->d_v_min != nullptr;
+  const Quant qz = make_quant(prm);
+  const bool f24 = (prm->i_V + prm->f_V - prm->f_a) <= 24;
+  const bool sat = prm->overflow_mode == SALT_SATURATE;
+
+  if (desc->kind == SALT_LAYER_CONV) {
+    ConvPlan pl;
+    rc = plan_conv(desc, prm, B, ext, &pl);
+    if (rc) return rc;
+    const size_t need = mask_bytes_conv(pl, desc, B, L);
+    if (workspace_bytes < need || (need && !d_workspace))
+      return fail(-1, "workspace of %zu bytes below the %zu needed", workspace_bytes, need);
+    if (!launch) return 0;
+    ConvArgs a;
+    a.g = conv_geom(desc, pl);
+    a.WPO = pl.WPO;
+    a.G = pl.G; a.Gi = pl.Gi; a.ncg = pl.ncg; a.nsb = pl.nsb; a.Rw = pl.Rw; a.R = pl.R;
+    a.qz = qz; a.table = prm->d_decay_table; a.q = prm->d_q; a.q_bits = prm->q_bits;
+    a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
+    a.cap = out->cap; a.fill_pads = out->fill_pads; a.merge = pl.merge;
+    a.out_t = out->d_times; a.out_s = out->d_src; a.out_n = out->d_n;
+    a.v_final = res->d_v_final; a.v_min = res->d_v_min; a.v_max = res->d_v_max;
+    a.stats = res->d_stats;
+    a.masks = static_cast<uint32_t*>(d_workspace);
+    if (!pl.merge) {
+      if ((rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
+      if ((rc = fill(reinterpret_cast<int32_t*>(a.masks), 0, need / 4, st))) return rc;
+    }
+    const int flags = (f24 ? kConvF24 : 0) | (sat ? kConvSat : 0) | (ext ? kConvExt : 0) |
+                      (prm->v_th_kind == SALT_VTH_PER_NEURON ? kConvVthN : 0);
+    HIP_TRY(launch_conv(a, pl, flags, B, st));
+    if (!pl.merge) {
+      CompactArgs c;
+      c.conv = 1; c.words = desc->oc * pl.WPO; c.WPO = pl.WPO; c.NC = pl.NC; c.OC = desc->oc;
+      c.HW = pl.HW; c.W = pl.W; c.HWin = a.g.HWin; c.Win = desc->w_in; c.K = desc->k;
+      c.S = desc->s; c.P = desc->p; c.L = L; c.times = in->d_times; c.src = in->d_src;
+      c.n_real = in->d_n_real; c.masks = a.masks; c.cap = out->cap;
+      c.fill_pads = out->fill_pads; c.out_t = out->d_times; c.out_s = out->d_src;
+      c.out_n = out->d_n;
+      hipLaunchKernelGGL(compact_kernel, dim3(B), dim3(kWave), 0, st, c);
+      HIP_TRY(hipGetLastError());
+    }
+    return 0;
+  }
+
+  FcPlan pl;
+  plan_fc(desc, &pl);
+  const size_t need = mask_bytes_fc(pl, B, L);
+  if (workspace_bytes < need || (need && !d_workspace))
+    return fail(-1, "workspace of %zu bytes below the %zu needed", workspace_bytes, need);
+  const size_t sw = (size_t)std::min(kWave * pl.npl, desc->n_out);
+  const size_t wbytes = (size_t)desc->n_in * sw * (prm->q_bits / 8);
+  const size_t tbytes = (size_t)(prm->n_table + 2) * 4;
+  const bool wlds = wbytes + tbytes <= kFcWeightLds;
+  const size_t lds = tbytes + (wlds ? wbytes : 0);
+  if (lds > (size_t)kLdsMax) return fail(-3, "decay table too long for LDS");
+  if (!launch) return 0;
+  FcArgs a;
+  a.n_in = desc->n_in; a.n_out = desc->n_out; a.words = pl.words;
+  a.qz = qz; a.table = prm->d_decay_table; a.qt = prm->d_q; a.q_bits = prm->q_bits;
+  a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
+  a.cap = out->cap; a.fill_pads = out->fill_pads; a.direct = pl.direct;
+  a.out_t = out->d_times; a.out_s = out->d_src; a.out_n = out->d_n;
+  a.v_final = res->d_v_final; a.v_min = res->d_v_min; a.v_max = res->d_v_max;
+  a.stats = res->d_stats;
+  a.masks = static_cast<uint32_t*>(d_workspace);
+  if (!pl.direct && (rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
+  const int flags = (f24 ? kFcF24 : 0) | (sat ? kFcSat : 0) | (wlds ? kFcWlds : 0);
+  const dim3 grid(pl.n_slices, B);
+  switch (prm->q_bits) {
+    case 8: HIP_TRY(launch_fc_q8(a, pl.npl, flags, grid, lds, st)); break;
+    case 16: HIP_TRY(launch_fc_q16(a, pl.npl, flags, grid, lds, st)); break;
+    default: HIP_TRY(launch_fc_q32(a, pl.npl, flags, grid, lds, st)); break;
+  }
+  if (!pl.direct) {
+    CompactArgs c;
+    memset(&c, 0, sizeof(c));
+    c.conv = 0; c.words = pl.words; c.L = L; c.times = in->d_times; c.src = in->d_src;
+    c.n_real = in->d_n_real; c.masks = a.masks; c.cap = out->cap;
+    c.fill_pads = out->fill_pads; c.out_t = out->d_times; c.out_s = out->d_src;
+    c.out_n = out->d_n;
+    hipLaunchKernelGGL(compact_kernel, dim3(B), dim3(kWave), 0, st, c);
+    HIP_TRY(hipGetLastError());
+  }
+  return 0;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ C-ABI
@@ -461,105 +569,10 @@ int32_t salt_layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
                            const salt_events_in* in, const salt_events_out* out,
                            const salt_layer_result* res, void* d_workspace,
                            size_t workspace_bytes, void* stream) {
-  int32_t rc = check_common(desc, prm);
+  int32_t rc = layer_forward(desc, prm, in, out, res, d_workspace, workspace_bytes, nullptr, 0);
   if (rc) return rc;
-  if (!in || !out || !res) return fail(-1, "null events or result descriptor");
-  const int B = in->B, L = in->L;
-  if (B < 0 || L < 0) return fail(-1, "invalid batch shape B=%d L=%d", B, L);
-  if (B > 65535) return fail(-1, "batch of %d streams above 65535", B);
-  if (B == 0) return 0;
-  if (!in->d_n_real || (L > 0 && (!in->d_times || !in->d_src)))
-    return fail(-1, "input events missing");
-  if (out->cap != desc->max_out_spikes) return fail(-1, "out.cap must equal max_out_spikes");
-  if (!out->d_n || (out->cap > 0 && (!out->d_times || !out->d_src)))
-    return fail(-1, "output stream buffers missing");
-  if (!res->d_stats) return fail(-1, "stats buffer missing");
-  if ((res->d_v_min == nullptr) != (res->d_v_max == nullptr))
-    return fail(-1, "give both or neither of v_min/v_max");
-  const bool ext = res->d_v_min != nullptr;
-  hipStream_t st = (hipStream_t)stream;
-  const Quant qz = make_quant(prm);
-  const bool f24 = (prm->i_V + prm->f_V - prm->f_a) <= 24;
-  const bool sat = prm->overflow_mode == SALT_SATURATE;
-
-  if (desc->kind == SALT_LAYER_CONV) {
-    ConvPlan pl;
-    rc = plan_conv(desc, prm, B, ext, &pl);
-    if (rc) return rc;
-    const size_t need = mask_bytes_conv(pl, desc, B, L);
-    if (workspace_bytes < need || (need && !d_workspace))
-      return fail(-1, "workspace of %zu bytes below the %zu needed", workspace_bytes, need);
-    ConvArgs a;
-    a.g = conv_geom(desc, pl);
-    a.WPO = pl.WPO;
-    a.G = pl.G; a.Gi = pl.Gi; a.ncg = pl.ncg; a.nsb = pl.nsb; a.Rw = pl.Rw; a.R = pl.R;
-    a.qz = qz; a.table = prm->d_decay_table; a.q = prm->d_q; a.q_bits = prm->q_bits;
-    a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
-    a.cap = out->cap; a.fill_pads = out->fill_pads; a.merge = pl.merge;
-    a.out_t = out->d_times; a.out_s = out->d_src; a.out_n = out->d_n;
-    a.v_final = res->d_v_final; a.v_min = res->d_v_min; a.v_max = res->d_v_max;
-    a.stats = res->d_stats;
-    a.masks = static_cast<uint32_t*>(d_workspace);
-    if (!pl.merge) {
-      if ((rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
-      if ((rc = fill(reinterpret_cast<int32_t*>(a.masks), 0, need / 4, st))) return rc;
-    }
-    const int flags = (f24 ? kConvF24 : 0) | (sat ? kConvSat : 0) | (ext ? kConvExt : 0) |
-                      (prm->v_th_kind == SALT_VTH_PER_NEURON ? kConvVthN : 0);
-    HIP_TRY(launch_conv(a, pl, flags, B, st));
-    if (!pl.merge) {
-      CompactArgs c;
-      c.conv = 1; c.words = desc->oc * pl.WPO; c.WPO = pl.WPO; c.NC = pl.NC; c.OC = desc->oc;
-      c.HW = pl.HW; c.W = pl.W; c.HWin = a.g.HWin; c.Win = desc->w_in; c.K = desc->k;
-      c.S = desc->s; c.P = desc->p; c.L = L; c.times = in->d_times; c.src = in->d_src;
-      c.n_real = in->d_n_real; c.masks = a.masks; c.cap = out->cap;
-      c.fill_pads = out->fill_pads; c.out_t = out->d_times; c.out_s = out->d_src;
-      c.out_n = out->d_n;
-      hipLaunchKernelGGL(compact_kernel, dim3(B), dim3(kWave), 0, st, c);
-      HIP_TRY(hipGetLastError());
-    }
-    return 0;
-  }
-
-  FcPlan pl;
-  plan_fc(desc, &pl);
-  const size_t need = mask_bytes_fc(pl, B, L);
-  if (workspace_bytes < need || (need && !d_workspace))
-    return fail(-1, "workspace of %zu bytes below the %zu needed", workspace_bytes, need);
-  FcArgs a;
-  a.n_in = desc->n_in; a.n_out = desc->n_out; a.words = pl.words;
-  a.qz = qz; a.table = prm->d_decay_table; a.qt = prm->d_q; a.q_bits = prm->q_bits;
-  a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
-  a.cap = out->cap; a.fill_pads = out->fill_pads; a.direct = pl.direct;
-  a.out_t = out->d_times; a.out_s = out->d_src; a.out_n = out->d_n;
-  a.v_final = res->d_v_final; a.v_min = res->d_v_min; a.v_max = res->d_v_max;
-  a.stats = res->d_stats;
-  a.masks = static_cast<uint32_t*>(d_workspace);
-  if (!pl.direct && (rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
-  const size_t sw = (size_t)std::min(kWave * pl.npl, desc->n_out);
-  const size_t wbytes = (size_t)desc->n_in * sw * (prm->q_bits / 8);
-  const size_t tbytes = (size_t)(prm->n_table + 2) * 4;
-  const bool wlds = wbytes + tbytes <= kFcWeightLds;
-  const size_t lds = tbytes + (wlds ? wbytes : 0);
-  if (lds > (size_t)kLdsMax) return fail(-3, "decay table too long for LDS");
-  const int flags = (f24 ? kFcF24 : 0) | (sat ? kFcSat : 0) | (wlds ? kFcWlds : 0);
-  const dim3 grid(pl.n_slices, B);
-  switch (prm->q_bits) {
-    case 8: HIP_TRY(launch_fc_q8(a, pl.npl, flags, grid, lds, st)); break;
-    case 16: HIP_TRY(launch_fc_q16(a, pl.npl, flags, grid, lds, st)); break;
-    default: HIP_TRY(launch_fc_q32(a, pl.npl, flags, grid, lds, st)); break;
-  }
-  if (!pl.direct) {
-    CompactArgs c;
-    memset(&c, 0, sizeof(c));
-    c.conv = 0; c.words = pl.words; c.L = L; c.times = in->d_times; c.src = in->d_src;
-    c.n_real = in->d_n_real; c.masks = a.masks; c.cap = out->cap;
-    c.fill_pads = out->fill_pads; c.out_t = out->d_times; c.out_s = out->d_src;
-    c.out_n = out->d_n;
-    hipLaunchKernelGGL(compact_kernel, dim3(B), dim3(kWave), 0, st, c);
-    HIP_TRY(hipGetLastError());
-  }
-  return 0;
+  return layer_forward(desc, prm, in, out, res, d_workspace, workspace_bytes,
+                       (hipStream_t)stream, 1);
 }
 
 int32_t salt_stream_hash(const float* d_times, const int32_t* d_src, const int32_t* d_n,
@@ -570,6 +583,87 @@ int32_t salt_stream_hash(const float* d_times, const int32_t* d_src, const int32
   hipLaunchKernelGGL(stream_hash_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, d_times,
                      d_src, d_n, cap, d_hash);
   HIP_TRY(hipGetLastError());
+  return 0;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Layer i's input: the caller's events for i = 0, else layer i-1's output stream.
+salt_events_in network_input(const salt_events_in* in, const salt_events_out* outs, int i) {
+  if (i == 0) return *in;
+  salt_events_in e;
+  e.B = in->B;
+  e.L = outs[i - 1].cap;
+  e.d_times = outs[i - 1].d_times;
+  e.d_src = outs[i - 1].d_src;
+  e.d_n_real = outs[i - 1].d_n;
+  return e;
+}
+
+int64_t layer_inputs(const salt_layer_desc* d) {
+  return d->kind == SALT_LAYER_CONV ? (int64_t)d->ic * d->h_in * d->w_in : d->n_in;
+}
+
+int64_t layer_neurons(const salt_layer_desc* d) {
+  if (d->kind != SALT_LAYER_CONV) return d->n_out;
+  const int64_t H = (d->h_in + 2 * d->p - d->k) / d->s + 1;
+  const int64_t W = (d->w_in + 2 * d->p - d->k) / d->s + 1;
+  return d->oc * H * W;
+}
+
+int32_t check_chain(int32_t n, const salt_layer_desc* descs, const salt_qparams* prms) {
+  if (n < 1 || !descs || !prms) return fail(-1, "network: need at least one layer");
+  for (int i = 1; i < n; ++i)
+    if (layer_inputs(&descs[i]) != layer_neurons(&descs[i - 1]))
+      return fail(-1, "network: layer %d takes %lld inputs, layer %d has %lld neurons", i,
+                  (long long)layer_inputs(&descs[i]), i - 1,
+                  (long long)layer_neurons(&descs[i - 1]));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t salt_network_workspace_size(int32_t n_layers, const salt_layer_desc* descs,
+                                    const salt_qparams* prms, int32_t B, int32_t L,
+                                    int32_t want_neuron_extremes, size_t* bytes) {
+  int32_t rc = check_chain(n_layers, descs, prms);
+  if (rc) return rc;
+  if (!bytes) return fail(-1, "null size pointer");
+  size_t most = 0;
+  for (int i = 0; i < n_layers; ++i) {
+    size_t b = 0;
+    const int32_t Li = i == 0 ? L : descs[i - 1].max_out_spikes;
+    rc = salt_layer_workspace_size(&descs[i], &prms[i], B, Li, want_neuron_extremes, &b);
+    if (rc) return rc;
+    most = std::max(most, b);
+  }
+  *bytes = most;
+  return 0;
+}
+
+int32_t salt_network_forward(int32_t n_layers, const salt_layer_desc* descs,
+                             const salt_qparams* prms, const salt_events_in* in,
+                             const salt_events_out* outs, const salt_layer_result* results,
+                             void* d_workspace, size_t workspace_bytes, void* stream) {
+  int32_t rc = check_chain(n_layers, descs, prms);
+  if (rc) return rc;
+  if (!in || !outs || !results) return fail(-1, "null events or result descriptors");
+  for (int i = 0; i < n_layers; ++i) {
+    const salt_events_in e = network_input(in, outs, i);
+    if ((rc = layer_forward(&descs[i], &prms[i], &e, &outs[i], &results[i], d_workspace,
+                            workspace_bytes, nullptr, 0)))
+      return rc;
+  }
+  for (int i = 0; i < n_layers; ++i) {
+    const salt_events_in e = network_input(in, outs, i);
+    if ((rc = layer_forward(&descs[i], &prms[i], &e, &outs[i], &results[i], d_workspace,
+                            workspace_bytes, (hipStream_t)stream, 1)))
+      return rc;
+  }
   return 0;
 }
 

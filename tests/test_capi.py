@@ -76,3 +76,52 @@ def test_unsupported_conv_geometry():
     rc = _lib.lib().salt_layer_workspace_size(ctypes.byref(d), ctypes.byref(_qp()), 1, 1, 0,
                                              ctypes.byref(size))
     assert rc == -3 and b"candidate" in _lib.lib().salt_last_error()
+
+
+def _chain(fc_n_out=4):
+    """conv 2x128x128 -> 32 3x3 s1 (partitioned: per-event spike masks) -> FC."""
+    d = (_lib.LayerDesc * 2)()
+    d[0].kind, d[0].ic, d[0].h_in, d[0].w_in, d[0].oc, d[0].k, d[0].s, d[0].p = 1, 2, 128, 128, 32, 3, 1, 0
+    d[0].max_queue_len, d[0].max_out_spikes = 100, 5000
+    d[1].kind, d[1].n_in, d[1].n_out, d[1].max_out_spikes = 0, 32 * 126 * 126, fc_n_out, 64
+    q = (_lib.QParams * 2)(_qp(), _qp())
+    return d, q
+
+
+@pytest.mark.parametrize("fc_n_out", [4, 3000])
+def test_network_workspace_is_the_largest_layer_workspace(fc_n_out):
+    d, q = _chain(fc_n_out)
+    lib = _lib.lib()
+    sizes = []
+    for i, L in enumerate((1000, d[0].max_out_spikes)):  # layer 1 reads layer 0's stream
+        s = ctypes.c_size_t()
+        assert lib.salt_layer_workspace_size(ctypes.byref(d[i]), ctypes.byref(q[i]), 64, L, 0,
+                                             ctypes.byref(s)) == 0
+        sizes.append(s.value)
+    size = ctypes.c_size_t()
+    assert lib.salt_network_workspace_size(2, d, q, 64, 1000, 0, ctypes.byref(size)) == 0
+    assert size.value == max(sizes) > 0
+    assert (sizes[1] > 0) == (fc_n_out > 64)  # several FC slices need spike masks too
+
+
+def test_network_rejects_mismatched_chain():
+    d, q = _chain()
+    d[1].n_in -= 1
+    size = ctypes.c_size_t()
+    assert _lib.lib().salt_network_workspace_size(2, d, q, 1, 1, 0, ctypes.byref(size)) == -1
+    assert b"layer 1 takes" in _lib.lib().salt_last_error()
+
+
+def test_network_checks_every_layer_before_launching():
+    """A bad parameter in the last layer fails the call before the first layer is
+    enqueued (no device is touched: the pointers here are placeholders)."""
+    d, q = _chain()
+    q[1] = _qp(f_a=16)
+    ev_in = _lib.EventsIn(B=2, L=10, d_times=8, d_src=8, d_n_real=8)
+    outs = (_lib.EventsOut * 2)(*[_lib.EventsOut(cap=d[i].max_out_spikes, d_times=8, d_src=8,
+                                                 d_n=8, fill_pads=0) for i in range(2)])
+    res = (_lib.LayerResult * 2)(*[_lib.LayerResult(d_v_final=8, d_v_min=None, d_v_max=None,
+                                                    d_stats=8) for _ in range(2)])
+    rc = _lib.lib().salt_network_forward(2, d, q, ctypes.byref(ev_in), outs, res, 8, 1 << 40,
+                                         None)
+    assert rc == -1 and b"MAX_SHIFT_BITS" in _lib.lib().salt_last_error()
