@@ -74,6 +74,12 @@ class ConvLayer:
     def with_capacity(self, capacity: Capacity) -> "ConvLayer":
         return replace(self, **capacity)
 
+    def with_chunk_size(self, chunk_size: int) -> "ConvLayer":
+        """New chunk_size with max_extra_steps reset to the value that always suffices
+        (salt_core/layers/conv.py:179-186)."""
+        return replace(self, chunk_size=chunk_size,
+                       max_extra_steps=safe_extra_steps(self.max_queue_len, chunk_size))
+
     def unflatten_neurons(self, values):
         """(n_neurons, ...) -> (oc, h_out, w_out, ...) (salt_core/layers/conv.py:104-112)."""
         check_leading_axis(values, self.n_neurons, "n_neurons")

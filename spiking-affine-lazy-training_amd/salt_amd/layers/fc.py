@@ -50,6 +50,10 @@ class FCLayer:
     def with_capacity(self, capacity: Capacity) -> "FCLayer":
         return replace(self, **capacity)
 
+    def with_chunk_size(self, chunk_size: int) -> "FCLayer":
+        """New chunk_size, max_extra_steps unchanged (salt_core/layers/fc.py:130-136)."""
+        return replace(self, chunk_size=chunk_size)
+
     def unflatten_neurons(self, values):
         check_leading_axis(values, self.n_out, "n_out")
         return values.reshape(self.n_out, 1, 1, *values.shape[1:])

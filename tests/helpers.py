@@ -46,3 +46,35 @@ def assert_layer_equal(gpu_out, ref, *, extremes=True, tag=""):
     np.testing.assert_array_equal(st[:, 1], ref["v_max"].max(axis=1), err_msg=f"{tag} stream vmax")
     if "needed_queue" in ref and st[:, 2].any():
         np.testing.assert_array_equal(st[:, 2], ref["needed_queue"], err_msg=f"{tag} needed queue")
+
+
+def encode_aer(x, y, c, t_us) -> bytes:
+    """Events -> N-MNIST 40-bit AER bytes (x, y, polarity<<7 | t[22:16], t[15:8], t[7:0]),
+    built byte by byte with Python integers."""
+    out = bytearray()
+    for xi, yi, ci, ti in zip(x, y, c, t_us):
+        xi, yi, ci, ti = int(xi), int(yi), int(ci), int(ti)
+        assert 0 <= ti < 1 << 23 and ci in (0, 1)
+        out += bytes([xi, yi, (ci << 7) | (ti >> 16), (ti >> 8) & 0xFF, ti & 0xFF])
+    return bytes(out)
+
+
+def write_nmnist_tree(root, per_digit_train=6, per_digit_test=3, seed=0, n_range=(40, 160)):
+    """A small N-MNIST-shaped tree: root/{Train,Test}/<digit>/<five digits>.bin with random
+    events (sorted microsecond times).  Returns {path: (x, y, c, t_us)}."""
+    import os
+    rng = np.random.default_rng(seed)
+    files = {}
+    for split, per in (("Train", per_digit_train), ("Test", per_digit_test)):
+        for d in range(10):
+            os.makedirs(os.path.join(root, split, str(d)), exist_ok=True)
+            for k in range(per):
+                n = int(rng.integers(*n_range))
+                x, y = rng.integers(0, 34, n), rng.integers(0, 34, n)
+                c = rng.integers(0, 2, n)
+                t = np.sort(rng.integers(0, 300_000, n))
+                path = os.path.join(root, split, str(d), f"{k * 7 + d:05d}.bin")
+                with open(path, "wb") as f:
+                    f.write(encode_aer(x, y, c, t))
+                files[path] = (x, y, c, t)
+    return files
