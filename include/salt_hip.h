@@ -170,6 +170,19 @@ int32_t salt_network_forward(int32_t n_layers, const salt_layer_desc* descs,
                              const salt_events_out* outs, const salt_layer_result* results,
                              void* d_workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Trace mode of one layer over a batch: per neuron and queue column, the register after
+ * the step, the step's spike / overflow flags and the time of the event it processed
+ * (run_layer_traced, salt_core/quant/scan.py:83-132; LayerForwardTrace and event_ms,
+ * salt_core/trace.py:13-55).  steps = max_queue_len for conv, L for FC; outputs are
+ * [B][n][steps]: d_v_steps int32, d_event_ms float32 (NaN for columns past the neuron's
+ * real events: catch-up and identity columns), d_flags uint8 (bit 0 spike, bit 1
+ * register overflow before write-back).  A debug path (one thread per neuron).
+ */
+int32_t salt_layer_trace(const salt_layer_desc* desc, const salt_qparams* prm,
+                         const salt_events_in* in, int32_t steps, int32_t* d_v_steps,
+                         float* d_event_ms, uint8_t* d_flags, void* stream);
+
 /* Order-sensitive 64-bit hash per stream, for streams too large to copy back.
  * With mix64 = the splitmix64 finaliser (add 0x9E3779B97F4A7C15, then xor-shift-multiply
  * by 0xBF58476D1CE4E5B9 and 0x94D049BB133111EB), entry i < min(n, cap) contributes

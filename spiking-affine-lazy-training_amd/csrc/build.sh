@@ -15,6 +15,7 @@ hipcc=/opt/rocm/bin/hipcc
 
 pids=()
 "$hipcc" "${flags[@]}" -c "$here/salt_hip.hip" -o "$obj/salt_hip.o" & pids+=($!)
+"$hipcc" "${flags[@]}" -c "$here/trace_kernel.hip" -o "$obj/trace.o" & pids+=($!)
 for n in 1 2 3 4 8; do
   "$hipcc" "${flags[@]}" -DSALT_NIT=$n -c "$here/conv_inst.hip" -o "$obj/conv_$n.o" & pids+=($!)
 done

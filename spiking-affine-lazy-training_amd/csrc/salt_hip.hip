@@ -22,6 +22,7 @@
 #include <string>
 
 #include "launch.hpp"
+#include "trace_kernel.hpp"
 
 using namespace salt;
 
@@ -573,6 +574,50 @@ int32_t salt_layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
   if (rc) return rc;
   return layer_forward(desc, prm, in, out, res, d_workspace, workspace_bytes,
                        (hipStream_t)stream, 1);
+}
+
+int32_t salt_layer_trace(const salt_layer_desc* desc, const salt_qparams* prm,
+                         const salt_events_in* in, int32_t steps, int32_t* d_v_steps,
+                         float* d_event_ms, uint8_t* d_flags, void* stream) {
+  int32_t rc = check_common(desc, prm);
+  if (rc) return rc;
+  if (!in) return fail(-1, "null events descriptor");
+  const int B = in->B, L = in->L;
+  if (B < 0 || L < 0) return fail(-1, "invalid batch shape B=%d L=%d", B, L);
+  if (B > 65535) return fail(-1, "batch of %d streams above 65535", B);
+  const bool conv = desc->kind == SALT_LAYER_CONV;
+  TraceArgs a;
+  memset(&a, 0, sizeof(a));
+  a.conv = conv;
+  if (conv) {
+    ConvPlan pl;
+    if ((rc = plan_conv(desc, prm, 1, false, &pl))) return rc;
+    a.IC = desc->ic; a.Hin = desc->h_in; a.Win = desc->w_in; a.K = desc->k; a.S = desc->s;
+    a.P = desc->p; a.H = pl.H; a.W = pl.W; a.mql = desc->max_queue_len;
+    a.n = desc->oc * pl.HW;
+    if (desc->max_queue_len < 1) return fail(-1, "max_queue_len must be at least 1");
+    if (steps != desc->max_queue_len)
+      return fail(-1, "conv trace: steps=%d must equal max_queue_len=%d", steps,
+                  desc->max_queue_len);
+  } else {
+    a.n_in = desc->n_in; a.n_out = desc->n_out;
+    a.n = desc->n_out;
+    if (steps != L) return fail(-1, "FC trace: steps=%d must equal the stream length L=%d", steps, L);
+  }
+  a.steps = steps;
+  if (B == 0 || a.n == 0 || steps == 0) return 0;
+  if (!in->d_n_real || (L > 0 && (!in->d_times || !in->d_src)))
+    return fail(-1, "input events missing");
+  if (!d_v_steps || !d_event_ms || !d_flags) return fail(-1, "trace output buffers missing");
+  a.sat = prm->overflow_mode == SALT_SATURATE;
+  a.qz = make_quant(prm);
+  a.table = prm->d_decay_table;
+  a.q = prm->d_q;
+  a.q_bits = prm->q_bits;
+  a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
+  a.v_steps = d_v_steps; a.event_ms = d_event_ms; a.flags = d_flags;
+  HIP_TRY(launch_trace(a, B, (hipStream_t)stream));
+  return 0;
 }
 
 int32_t salt_stream_hash(const float* d_times, const int32_t* d_src, const int32_t* d_n,

@@ -64,6 +64,8 @@ SIGNATURES = {
                             ctypes.POINTER(EventsIn), ctypes.POINTER(EventsOut),
                             ctypes.POINTER(LayerResult), _p, ctypes.c_size_t, _p], _i32),
     "salt_stream_hash": ([_p, _p, _p, _i32, _i32, _p, _p], _i32),
+    "salt_layer_trace": ([ctypes.POINTER(LayerDesc), ctypes.POINTER(QParams),
+                          ctypes.POINTER(EventsIn), _i32, _p, _p, _p, _p], _i32),
     "salt_network_workspace_size": ([_i32, ctypes.POINTER(LayerDesc), ctypes.POINTER(QParams),
                                      _i32, _i32, _i32, ctypes.POINTER(ctypes.c_size_t)], _i32),
     "salt_network_forward": ([_i32, ctypes.POINTER(LayerDesc), ctypes.POINTER(QParams),

@@ -7,7 +7,7 @@ class LayerOutput(NamedTuple):
     stream: Any   # EventStream fed to the next layer
     result: Any   # QuantLayerResult
     diag: Any     # LayerDiag
-    trace: Any    # always None: the trace mode is not part of this path
+    trace: Any    # LayerForwardTrace when forward ran with trace=True, else None
 
 
 def base_scan_steps(queue_len: int, chunk_size: int) -> int:

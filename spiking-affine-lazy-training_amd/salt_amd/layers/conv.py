@@ -93,10 +93,11 @@ class ConvLayer:
     def forward(self, params, in_stream, *, backend=None, trace: bool = False) -> LayerOutput:
         """Integer forward of this layer over a (batched) EventStream."""
         from salt_amd.quant.backend import resolve_backend
+        be = resolve_backend(backend)
+        out = be.layer_forward(self, params, in_stream)
         if trace:
-            raise NotImplementedError("trace=True (per-step register trajectories) is not "
-                                      "part of the GPU integer path")
-        return resolve_backend(backend).layer_forward(self, params, in_stream)
+            out = out._replace(trace=be.layer_trace(self, params, in_stream))
+        return out
 
 
 @dataclass(frozen=True)

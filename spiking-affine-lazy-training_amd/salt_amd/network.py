@@ -60,7 +60,7 @@ class NetworkOutput(NamedTuple):
     """run_network's output (salt_core/network.py:57-67)."""
     results: tuple
     diags: tuple
-    traces: None
+    traces: tuple | None  # LayerForwardTrace per layer when run with trace=True
     fits: torch.Tensor  # bool: every layer with a capacity held this input
 
     @property
@@ -87,15 +87,14 @@ def check_layer_connections(layers: Sequence) -> None:
 
 def run_network(layers: Sequence, weights: Sequence, input_stream: EventStream, *,
                 backend: QuantBackend | None = None, trace: bool = False) -> NetworkOutput:
-    """Chain layers, each output stream feeding the next (salt_core/network.py:93-122)."""
-    if trace:
-        raise NotImplementedError("trace=True is not part of the GPU integer path")
+    """Chain layers, each output stream feeding the next (salt_core/network.py:93-122).
+    trace: also collect every layer's step-by-step trajectories (LayerForwardTrace)."""
     backend = resolve_backend(backend)
     check_layer_connections(layers)
     stream = input_stream
     outputs = []
     for layer, params in zip(layers, weights):
-        out = layer.forward(params, stream, backend=backend)
+        out = layer.forward(params, stream, backend=backend, trace=trace)
         outputs.append(out)
         stream = out.stream
     fits = None
@@ -104,7 +103,8 @@ def run_network(layers: Sequence, weights: Sequence, input_stream: EventStream, 
             f = layer.capacity.fits(out.diag)
             fits = f if fits is None else fits & f
     return NetworkOutput(results=tuple(o.result for o in outputs),
-                         diags=tuple(o.diag for o in outputs), traces=None, fits=fits)
+                         diags=tuple(o.diag for o in outputs),
+                         traces=tuple(o.trace for o in outputs) if trace else None, fits=fits)
 
 
 @dataclass(frozen=True)

@@ -326,6 +326,40 @@ class QuantBackend:
         return LayerOutput(stream=stream, result=result, diag=diag, trace=None)
 
 
+    def layer_trace(self, layer, params: QuantizedLayerParams, in_stream: EventStream):
+        """The layer's step-by-step trajectories over a (batched) EventStream
+        (salt_core/quant/scan.py:83-95 under trace=True): salt_layer_trace."""
+        from salt_amd.trace import LayerForwardTrace
+        round_mode = RoundMode(self.round_mode)
+        single = in_stream.event_times.dim() == 1
+        times = _batched(in_stream.event_times).to(torch.float32).contiguous()
+        src = _batched(in_stream.event_source_idx).to(torch.int32).contiguous()
+        n_real = in_stream.n_real_events.reshape(-1).to(torch.int32).contiguous()
+        if not times.is_cuda:
+            raise ValueError("the event stream must live on the GPU")
+        dp = self.device_params(layer, params, times.device)
+        B, L = times.shape
+        steps = int(layer.max_queue_len) if hasattr(layer, "oc") else L
+        n = layer.n_neurons
+        v_steps = torch.empty((B, n, steps), dtype=torch.int32, device=times.device)
+        event_ms = torch.empty((B, n, steps), dtype=torch.float32, device=times.device)
+        flags = torch.empty((B, n, steps), dtype=torch.uint8, device=times.device)
+        desc = layer_desc(layer)
+        qp = qparams(dp, round_mode)
+        ev_in = _lib.EventsIn(B=B, L=L, d_times=times.data_ptr(), d_src=src.data_ptr(),
+                              d_n_real=n_real.data_ptr())
+        _lib.check(_lib.lib().salt_layer_trace(ctypes.byref(desc), ctypes.byref(qp),
+                                               ctypes.byref(ev_in), steps, v_steps.data_ptr(),
+                                               event_ms.data_ptr(), flags.data_ptr(),
+                                               _lib.current_stream()),
+                   f"salt_layer_trace({layer.name})")
+        tr = LayerForwardTrace(spike_mask=(flags & 1).bool(), v_steps=v_steps,
+                               event_ms=event_ms, overflowed=(flags & 2).bool())
+        if single:
+            tr = LayerForwardTrace(*(x[0] for x in tr))
+        return tr
+
+
 _PARAM_CACHE: dict = {}
 QUANT = QuantBackend()
 

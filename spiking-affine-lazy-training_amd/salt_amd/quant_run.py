@@ -181,11 +181,58 @@ def min_extra_bits(network, decoder, params, round_mode, raw, batch_size: int, p
     return extra, rounds
 
 
+MAX_OVERFLOW_EVENTS = 50  # example/quant_run.py:20-21
+
+
+def _neuron_position(layer, neuron: int) -> tuple[int, int, int]:
+    """Neuron id -> (channel, y, x); FC neurons are (neuron, 0, 0)."""
+    shape = (layer.oc, layer.h_out, layer.w_out) if hasattr(layer, "oc") else (layer.n_out, 1, 1)
+    return tuple(int(v) for v in np.unravel_index(neuron, shape))
+
+
+def overflow_events(network: Network, params, round_mode: RoundMode | str, raw: InputEvents,
+                    out: QuantSplitOutput) -> list[dict]:
+    """Where registers overflowed: for every overflowing (sample, layer, neuron), its
+    first overflowing step, from a traced re-run of that sample
+    (example/quant_run.py:180-210).  At most MAX_OVERFLOW_EVENTS entries.  v_before /
+    v_after: the register before and after that step (0 after a spike); true_min /
+    true_max: the neuron's extremes of the value before write-back over the sample."""
+    backend = QuantBackend(round_mode=round_mode)
+    events = []
+    for i in np.nonzero(out.overflowed.any(axis=1))[0]:
+        one = InputEvents(*(np.asarray(a)[int(i)] for a in raw))
+        output = network.apply(params, one, backend=backend, trace=True)
+        for layer, p, result, trace in zip(network.layers, params, output.results, output.traces):
+            overflowed = trace.overflowed.cpu().numpy()
+            if not overflowed.any():
+                continue
+            v_steps = trace.v_steps.cpu().numpy()
+            event_ms = trace.event_ms.cpu().numpy()
+            spikes = trace.spike_mask.cpu().numpy()
+            vmin = result.v_unfitted_min.cpu().numpy()
+            vmax = result.v_unfitted_max.cpu().numpy()
+            w = int(p.i_V) + int(p.f_V)
+            for neuron in np.nonzero(overflowed.any(axis=1))[0]:
+                step = int(np.argmax(overflowed[neuron]))
+                channel, y, x = _neuron_position(layer, int(neuron))
+                events.append({
+                    "sample": int(i), "layer": layer.name, "channel": channel, "y": y, "x": x,
+                    "time_ms": float(event_ms[neuron, step]),
+                    "v_before": int(v_steps[neuron, step - 1]) if step > 0 else 0,
+                    "v_after": int(v_steps[neuron, step]),
+                    "spiked": bool(spikes[neuron, step]),
+                    "true_min": int(vmin[neuron]), "true_max": int(vmax[neuron]),
+                    "register_range": [-2 ** (w - 1), 2 ** (w - 1) - 1]})
+                if len(events) >= MAX_OVERFLOW_EVENTS:
+                    return events
+    return events
+
+
 def overflow_summary(network, decoder, params, round_mode, raw, batch_size: int, policies: dict,
                      out, *, device=None) -> dict:
     """Overflowed samples per layer, headroom and, unless a layer saturates, the fewest
-    extra register bits that remove every overflow (example/quant_run.py:213-240,
-    without the per-neuron overflow_events listing)."""
+    extra register bits that remove every overflow and where the overflows happened
+    (example/quant_run.py:213-240)."""
     names = [layer.name for layer in network.layers]
     summary = {"overflowed_samples": {n: int(out.overflowed[:, i].sum()) for i, n in enumerate(names)},
                "headroom_bits": dict(zip(names, headroom_bits(params, out)))}
@@ -193,4 +240,5 @@ def overflow_summary(network, decoder, params, round_mode, raw, batch_size: int,
         return summary
     extra, rounds = min_extra_bits(network, decoder, params, round_mode, raw, batch_size,
                                    policies, out, device=device)
-    return {**summary, "min_extra_bits": dict(zip(names, extra)), "min_extra_bits_rounds": rounds}
+    return {**summary, "min_extra_bits": dict(zip(names, extra)), "min_extra_bits_rounds": rounds,
+            "overflow_events": overflow_events(network, params, round_mode, raw, out)}

@@ -157,3 +157,35 @@ def test_check_and_eval_on_a_model_folder(tmp_path):
     assert os.path.exists(folder / "eval" / "test.yaml")
     with np.load(folder / "eval" / "test_outputs.npz") as npz:
         assert npz["preds"].shape == (20,) and npz["labels"].shape == (20,)
+
+
+def test_overflow_events_match_the_queue_restatement():
+    """overflow_events re-runs each overflowing sample in trace mode; every listed event
+    (first overflowing step of a neuron) equals the queue restatement's trajectory of that
+    layer on the same input stream."""
+    from oracle import queue_ref as Q
+    from salt_amd.quant_run import MAX_OVERFLOW_EVENTS, overflow_events
+    net, params = _net(mql=160)
+    raw = _raw(2, 20)
+    out = quant_forward_split(net, MembraneRegressionDecoder(), params, "round", raw, 7, device=DEV)
+    assert not out.truncated.any() and out.overflowed[:, :2].sum() == 0
+    print("overflow_events", flush=True)
+    events = overflow_events(net, params, "round", raw, out)
+    refs = oracle_network(net, params, raw, "round")
+    fc, p = net.layers[2], params[2]
+    want = []
+    for i in np.nonzero(out.overflowed.any(axis=1))[0]:
+        n_in = int(refs[1]["out_n"][i])
+        r = Q.fc_forward(p.q, p.decay_table_int, None, p.f_a, p.f_V, p.i_V,
+                         refs[1]["out_times"][i], refs[1]["out_src"][i], n_in, 4096,
+                         round_mode="round", overflow_mode="wrap")
+        for neuron in np.nonzero(r["overflowed"].any(axis=1))[0]:
+            step = int(np.argmax(r["overflowed"][neuron]))
+            want.append({"sample": int(i), "layer": "out", "channel": int(neuron), "y": 0, "x": 0,
+                         "time_ms": float(refs[1]["out_times"][i][step]),
+                         "v_before": int(r["v_steps"][neuron, step - 1]) if step > 0 else 0,
+                         "v_after": int(r["v_steps"][neuron, step]), "spiked": False,
+                         "true_min": int(refs[2]["v_min"][i, neuron]),
+                         "true_max": int(refs[2]["v_max"][i, neuron]),
+                         "register_range": [-1024, 1023]})
+    assert events == want[:MAX_OVERFLOW_EVENTS] and len(events) > 0
