@@ -189,3 +189,31 @@ def test_overflow_events_match_the_queue_restatement():
                          "true_max": int(refs[2]["v_max"][i, neuron]),
                          "register_range": [-1024, 1023]})
     assert events == want[:MAX_OVERFLOW_EVENTS] and len(events) > 0
+
+
+def test_converted_params_run_through_the_quantized_network():
+    """build_quantized_params output is directly usable (salt_core/tests/
+    test_quant_convert.py:96-107): conv 2x2x2 -> FC 8 -> 2, four events."""
+    from salt_amd import run_network
+    from salt_amd.quant.convert import LayerQuantSpec, build_quantized_params
+    from salt_amd.stream import EventStream
+    conv = ConvLayer(name="conv", ic=2, h_in=2, w_in=2, oc=2, k=1, s=1, p=0, init_k=5.0,
+                     tau=16.0, v_th=1.0, chunk_size=1, max_queue_len=8, max_out_spikes=64)
+    fc = FCLayer(name="out", n_in=8, n_out=2, init_k=5.0, tau=16.0, v_th=1e9)
+    params = build_quantized_params(
+        [conv, fc], (np.array([0.375, 0.125, -1.0, 0.25], np.float32).reshape(2, 2, 1, 1),
+                     np.linspace(-0.5, 0.3, 16, dtype=np.float32).reshape(2, 8)),
+        [LayerQuantSpec(bits=4, f_a=8, f_V=4), LayerQuantSpec(bits=4, f_a=8, f_V=4, fires=False)],
+        [np.array([2.0, 0.5]), np.array([3.0, 1.0])])
+    t = torch.arange(1.0, 5.0, device=DEV)
+    stream = EventStream(event_times=t, event_source_idx=torch.arange(4, dtype=torch.int32, device=DEV),
+                         event_gain=torch.ones(4, device=DEV),
+                         n_real_events=torch.tensor(4, dtype=torch.int32, device=DEV))
+    out = run_network([conv, fc], params, stream, backend=QuantBackend())
+    assert tuple(out.last.v_final.shape) == (2,)
+    assert bool(conv.capacity.fits(out.diags[0]))
+    # the same run on the CPU oracle
+    raw = InputEvents(np.arange(1.0, 5.0, dtype=np.float32)[None], np.arange(4, dtype=np.int32)[None],
+                      np.array([4], np.int32))
+    refs = oracle_network(Network((2, 2, 2), [conv, fc]), params, raw, "round")
+    np.testing.assert_array_equal(out.last.v_final.cpu().numpy(), refs[-1]["v_final"][0])
