@@ -14,9 +14,10 @@ namespace {
 template <int NIT, int F>
 hipError_t conv_entry(const ConvArgs& a, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
   constexpr bool kF24 = (F & kConvF24) != 0, kSat = (F & kConvSat) != 0,
-                 kExt = (F & kConvExt) != 0, kVthN = (F & kConvVthN) != 0;
+                 kExt = (F & kConvExt) != 0, kVthN = (F & kConvVthN) != 0,
+                 kM32 = (F & kConvM32) != 0, kNoTrunc = (F & kConvNoTrunc) != 0;
   static bool attr_set = false;
-  auto fn = conv_layer_kernel<NIT, kF24, kSat, kExt, kVthN>;
+  auto fn = conv_layer_kernel<NIT, kF24, kSat, kExt, kVthN, kM32, kNoTrunc>;
   return launch_with_lds(reinterpret_cast<const void*>(fn), fn, &attr_set, grid, block, lds, st,
                          a);
 }
@@ -35,8 +36,9 @@ constexpr std::array<ConvFn, sizeof...(F)> conv_table(std::integer_sequence<int,
 
 hipError_t SALT_CAT(launch_conv_nit, SALT_NIT)(const ConvArgs& a, int flags, dim3 grid,
                                                dim3 block, size_t lds, hipStream_t st) {
-  static constexpr auto table = conv_table<SALT_NIT>(std::make_integer_sequence<int, 16>{});
-  return table[flags & 15](a, grid, block, lds, st);
+  static constexpr auto table =
+      conv_table<SALT_NIT>(std::make_integer_sequence<int, kConvFlagCombos>{});
+  return table[flags & (kConvFlagCombos - 1)](a, grid, block, lds, st);
 }
 
 }  // namespace salt

@@ -133,7 +133,11 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int ncg, int nsb
   return l;
 }
 
-// Per-lane constants and LDS pointers of one wave (see the file comment).
+// Per-lane constants and LDS pointers of one wave (see the file comment).  The event
+// loop addresses LDS by byte offsets from the start of the work-group's LDS (where the
+// decay table sits): records hold an event's position and code bases pre-scaled to
+// bytes, and the lane constants below fold in this wave's region, so an address is one
+// add (or shift-add) and a select.
 struct ConvLane {
   int4* rec;
   int2* rec1;
@@ -151,13 +155,24 @@ struct ConvLane {
   int v_spare, q_zero, tc_spare;  // this lane's spare register word, zero code, spare entry
   int GiVS, GiQS;
   int cand, oc_lane, mql, ntab;
+  // byte offsets from the LDS base, for the event loop
+  int extb;                     // decay table
+  int lvb, lqb, ltb;            // register, code, (time, count) entry of an event's base
+  int v_spare_b, q_zero_b, tc_spare_b;
+  int GiVSb, GiQSb;             // per iteration
+  int dmn, dmx, dth;            // register array -> extremes / per-neuron thresholds
 };
 
+// The LDS address of a pointer into the work-group's LDS.
+__device__ __forceinline__ uint32_t lds_addr(const int32_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int32_t*)p;
+}
+
 // Lane constants for a wave of Gi slots per iteration over a band of PWs positions
-// (slot strides VS / QS), whose first channel is oc0.
+// (slot strides VS / QS), whose first channel is oc0.  base: the work-group's LDS.
 __device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, int lane,
                                                 int Gi, int VS, int QS, int PWs, int oc0,
-                                                int ntab) {
+                                                int ntab, const int32_t* base) {
   const int slot0 = lane / g.NC2;
   c.cand = lane - slot0 * g.NC2;
   const int dy = c.cand / g.NC, dx = c.cand - (c.cand / g.NC) * g.NC;
@@ -176,11 +191,46 @@ __device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, 
   c.oc_lane = oc0 + slot0;
   c.mql = g.mql;
   c.ntab = ntab;
+  const int vw = (int)(c.Vs - base), qw = (int)(c.qs - base);
+  const int tw = (int)(reinterpret_cast<const int32_t*>(c.tc) - base);
+  const int b0 = (int)lds_addr(base);
+  c.lvb = b0 + (vw + c.lv) * 4;
+  c.lqb = b0 + (qw + c.lq) * 4;
+  c.ltb = b0 + tw * 4 + c.lp * 8;
+  c.v_spare_b = b0 + (vw + c.v_spare) * 4;
+  c.q_zero_b = b0 + (qw + c.q_zero) * 4;
+  c.tc_spare_b = b0 + tw * 4 + c.tc_spare * 8;
+  c.extb = (int)lds_addr(c.ext);
+  c.GiVSb = c.GiVS * 4;
+  c.GiQSb = c.GiQS * 4;
+  c.dmn = (int)(c.mn - c.Vs) * 4;
+  c.dmx = (int)(c.mx - c.Vs) * 4;
+  c.dth = (int)(c.th - c.Vs) * 4;
+}
+
+// LDS access by byte address (the base is folded into the lane constants once, so the
+// event loop adds nothing to an address).
+template <typename T>
+__device__ __forceinline__ T lds_ld(int addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) T*>((uintptr_t)(uint32_t)addr);
+}
+template <typename T>
+__device__ __forceinline__ void lds_st(int addr, T v) {
+  *reinterpret_cast<__attribute__((address_space(3))) T*>((uintptr_t)(uint32_t)addr) = v;
+}
+// (time, count) entries as one 64-bit word.
+__device__ __forceinline__ int2 lds_ld_tc(int addr) {
+  const uint64_t w = lds_ld<uint64_t>(addr);
+  return make_int2((int)(uint32_t)w, (int)(uint32_t)(w >> 32));
+}
+__device__ __forceinline__ void lds_st_tc(int addr, int t, int cnt) {
+  lds_st<uint64_t>(addr, ((uint64_t)(uint32_t)cnt << 32) | (uint32_t)t);
 }
 
 // Decodes the events of one chunk (connectivity/conv.py:15-43), one per lane (time tv,
 // source sv, index j; real when j < n_eff and sv >= 0), against the rows [r0, r0+rn):
-// records for the events with a candidate there, compacted in order.  Returns their
+// records {time, position base * 4, code base * 4, candidate mask low} + {mask high,
+// event index} for the events with a candidate there, compacted in order.  Returns their
 // number; oy0/ox0 = the event's first candidate row and column.
 __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c, int tv,
                                            int sv, int j, int n_eff, int r0, int rn, int& oy0,
@@ -211,7 +261,7 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
   const uint64_t relm = __ballot(rel);
   if (rel) {
     const int slot = lanes_below(relm);
-    c.rec[slot] = make_int4(tv, p0, q0, (int)(uint32_t)m);
+    c.rec[slot] = make_int4(tv, p0 * 4, q0 * 4, (int)(uint32_t)m);
     c.rec1[slot] = make_int2((int)(uint32_t)(m >> 32), j);
   }
   return __popcll(relm);
@@ -229,63 +279,79 @@ struct ConvSink {
 
 // The events of one decoded chunk, in order (salt_core/quant/scan.py:22-52 per update).
 // kStage: stage the spike ballots for the work-group's merge; kMask: set spike bits in
-// global memory.
-template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, int MODE>
+// global memory.  M32: candidate masks fit 32 bits (NC^2 <= 32).  NOTRUNC: no position
+// can hold max_queue_len events (max_queue_len >= the stream length), so every candidate
+// event is a real queue column.
+template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, int MODE, bool M32, bool NOTRUNC>
 __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
                                             const int (&vtc)[NIT], int n_ev, int base,
                                             const ConvSink& sk, int& vmin_l, int& vmax_l) {
   if (n_ev == 0) return;
+  constexpr bool kRec1 = !M32 || MODE == kMask;  // the loop needs the second record word
   // kStage: lane e of sg_lo/sg_hi[it] collects event e's spike ballot; they are
   // stored once per chunk.
   uint32_t sg_lo[NIT], sg_hi[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) { sg_lo[it] = 0; sg_hi[it] = 0; }
   const int fa = qz.fa, rc = qz.rc;
+  const uint32_t nt1 = (uint32_t)c.ntab + 1u;
   const int lane = threadIdx.x & (kWave - 1);
+  const uint32_t lm32 = (uint32_t)c.lm;
+  auto covers = [&](const int4& r, const int2& r1) -> bool {
+    if (M32) return ((uint32_t)r.w & lm32) != 0u;
+    return ((((uint64_t)(uint32_t)r1.x << 32) | (uint32_t)r.w) & c.lm) != 0;
+  };
   // Software pipeline: the record of event e+1 and its positions' (time, count) are
   // read while event e is processed (after e's own count/time write, so they are
   // current), which leaves one LDS round trip per event: decay code, registers, codes.
   int4 r = c.rec[0];
-  int2 r1 = c.rec1[0];
-  bool vc = ((((uint64_t)(uint32_t)r1.x << 32) | (uint32_t)r.w) & c.lm) != 0;
-  int2 st = c.tc[vc ? r.y + c.lp : c.tc_spare];
+  int2 r1 = kRec1 ? c.rec1[0] : make_int2(0, 0);
+  bool vc = covers(r, r1);
+  int2 st = lds_ld_tc(vc ? 2 * r.y + c.ltb : c.tc_spare_b);
   for (int e = 0; e < n_ev; ++e) {
     const bool more = e + 1 < n_ev;
-    const int4 rn = c.rec[more ? e + 1 : e];
-    const int2 rn1 = c.rec1[more ? e + 1 : e];
-    const int pa = r.y + c.lp;
+    const int en = more ? e + 1 : e;
+    const int4 rn = c.rec[en];
+    const int2 rn1 = kRec1 ? c.rec1[en] : make_int2(0, 0);
+    const int pab = 2 * r.y + c.ltb;
     // A position whose queue is full (max_queue_len real columns) drops the event and
     // its time (connectivity/conv.py:57-99 truncates the queue).
-    const bool act = vc && st.y < c.mql;
-    c.tc[(vc && c.first) ? pa : c.tc_spare] = make_int2(act ? r.x : st.x, st.y + 1);
-    const int A = c.ext[decay_slot(r.x - st.x, c.ntab)];
-    const int va = act ? r.y + c.lv : c.v_spare;
-    const int qa = act ? r.z + c.lq : c.q_zero;
+    const bool act = NOTRUNC ? vc : (vc && st.y < c.mql);
+    lds_st_tc((vc && c.first) ? pab : c.tc_spare_b, NOTRUNC ? r.x : (act ? r.x : st.x),
+              st.y + 1);
+    // Decay code: dt = 0 -> identity, 1..n -> table, > n -> 0 (an unsigned clamp).
+    const int A = lds_ld<int32_t>(c.extb + (int)(min((uint32_t)(r.x - st.x), nt1) << 2));
+    const int va = act ? r.y + c.lvb : c.v_spare_b;
+    const int qa = act ? r.z + c.lqb : c.q_zero_b;
     int v[NIT], qv[NIT], vt[NIT], mnv[NIT], mxv[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-      v[it] = c.Vs[va + it * c.GiVS];
-      qv[it] = c.qs[qa + it * c.GiQS];
-      vt[it] = VTHN ? c.th[va + it * c.GiVS] : vtc[it];
-      if (EXT) { mnv[it] = c.mn[va + it * c.GiVS]; mxv[it] = c.mx[va + it * c.GiVS]; }
+      v[it] = lds_ld<int32_t>(va + it * c.GiVSb);
+      qv[it] = lds_ld<int32_t>(qa + it * c.GiQSb);
+      vt[it] = VTHN ? lds_ld<int32_t>(va + it * c.GiVSb + c.dth) : vtc[it];
+      if (EXT) {
+        mnv[it] = lds_ld<int32_t>(va + it * c.GiVSb + c.dmn);
+        mxv[it] = lds_ld<int32_t>(va + it * c.GiVSb + c.dmx);
+      }
     }
-    const bool vcn = more && ((((uint64_t)(uint32_t)rn1.x << 32) | (uint32_t)rn.w) & c.lm) != 0;
-    const int2 stn = c.tc[vcn ? rn.y + c.lp : c.tc_spare];
+    const bool vcn = more && covers(rn, rn1);
+    const int2 stn = lds_ld_tc(vcn ? 2 * rn.y + c.ltb : c.tc_spare_b);
     uint64_t bal[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       const int32_t d = decay_mul<F24>(v[it], A, fa, rc);
       const int32_t u = (int32_t)((uint32_t)d + (uint32_t)qv[it]);  // codes hold q*2^f_V
       const int32_t f = fit_bits<SAT>(u, qz);
-      const bool fi = f >= vt[it];
-      c.Vs[va + it * c.GiVS] = fi ? 0 : f;
+      const bool keep = f < vt[it];
+      lds_st<int32_t>(va + it * c.GiVSb, keep ? f : 0);
       vmin_l = min(vmin_l, u);
       vmax_l = max(vmax_l, u);
       if (EXT) {
-        c.mn[va + it * c.GiVS] = min(mnv[it], u);
-        c.mx[va + it * c.GiVS] = max(mxv[it], u);
+        lds_st<int32_t>(va + it * c.GiVSb + c.dmn, min(mnv[it], u));
+        lds_st<int32_t>(va + it * c.GiVSb + c.dmx, max(mxv[it], u));
       }
-      bal[it] = __ballot(fi);
+      // The spikes are the active lanes that did not keep their value: one compare.
+      bal[it] = __ballot(true) & ~__ballot(keep);
     }
     const bool mine = lane == e;
 #pragma unroll
@@ -350,7 +416,7 @@ __device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane& c, i
   return wave_max(maxcnt);
 }
 
-template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN>
+template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, bool M32, bool NOTRUNC>
 __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvArgs a) {
   extern __shared__ int32_t smem[];
   const ConvGeom& g = a.g;
@@ -425,7 +491,7 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   for (int i = lane; i < lay.tcn; i += kWave) c.tc[i] = make_int2(0, 0);
   __syncthreads();
 
-  conv_lane_setup(c, g, lane, Gi, VS, QS, PWs, oc0, qz.n_table);
+  conv_lane_setup(c, g, lane, Gi, VS, QS, PWs, oc0, qz.n_table, smem);
   int vtc[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) vtc[it] = vthc[min(it * Gi + c.oc_lane - oc0, Gp - 1)];
@@ -459,8 +525,8 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
       for (int i = lane; i < kWave * NIT; i += kWave) c.stg[i] = 0;
     __syncthreads();
     if (a.merge) {
-      conv_events<NIT, F24, SAT, EXT, VTHN, kStage>(qz, c, vtc, n_ev, base, sk, vmin_l,
-                                                     vmax_l);
+      conv_events<NIT, F24, SAT, EXT, VTHN, kStage, M32, NOTRUNC>(qz, c, vtc, n_ev, base,
+                                                                   sk, vmin_l, vmax_l);
       __syncthreads();  // every wave's ballots of this chunk are staged
       if (wv == 0) {
         // Walk (event, channel group, iteration, bit) = (event, ascending neuron id);
@@ -504,8 +570,8 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
       }
       __syncthreads();  // the staging and records are rewritten by the next chunk
     } else {
-      conv_events<NIT, F24, SAT, EXT, VTHN, kMask>(qz, c, vtc, n_ev, base, sk, vmin_l,
-                                                    vmax_l);
+      conv_events<NIT, F24, SAT, EXT, VTHN, kMask, M32, NOTRUNC>(qz, c, vtc, n_ev, base,
+                                                                  sk, vmin_l, vmax_l);
       __syncthreads();  // records are rewritten by the next chunk
     }
   }
