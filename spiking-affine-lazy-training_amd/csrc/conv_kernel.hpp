@@ -267,6 +267,21 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
   return __popcll(relm);
 }
 
+// lo/hi of lane e <- the wave-uniform 64-bit value v; other lanes keep theirs.  Two
+// moves under a one-lane exec mask (saved and restored inside the block), which is
+// fewer vector instructions than comparing every lane with e and selecting.
+__device__ __forceinline__ void stage_to_lane(uint32_t& lo, uint32_t& hi, uint64_t v, int e) {
+  uint64_t lane_mask, saved;
+  asm volatile(
+      "s_lshl_b64 %[m], 1, %[e]\n\t"
+      "s_and_saveexec_b64 %[sv], %[m]\n\t"
+      "v_mov_b32 %[lo], %[vlo]\n\t"
+      "v_mov_b32 %[hi], %[vhi]\n\t"
+      "s_mov_b64 exec, %[sv]"
+      : [lo] "+v"(lo), [hi] "+v"(hi), [m] "=&s"(lane_mask), [sv] "=&s"(saved)
+      : [e] "s"(e), [vlo] "s"((uint32_t)v), [vhi] "s"((uint32_t)(v >> 32)));
+}
+
 // Where a wave's spikes go.
 enum ConvMode { kStage = 0, kMask = 1 };
 
@@ -307,13 +322,13 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   int4 r = c.rec[0];
   int2 r1 = kRec1 ? c.rec1[0] : make_int2(0, 0);
   bool vc = covers(r, r1);
-  int2 st = lds_ld_tc(vc ? 2 * r.y + c.ltb : c.tc_spare_b);
+  int pab = 2 * r.y + c.ltb;  // this lane's (time, count) entry for the current event
+  int2 st = lds_ld_tc(vc ? pab : c.tc_spare_b);
   for (int e = 0; e < n_ev; ++e) {
     const bool more = e + 1 < n_ev;
     const int en = more ? e + 1 : e;
     const int4 rn = c.rec[en];
     const int2 rn1 = kRec1 ? c.rec1[en] : make_int2(0, 0);
-    const int pab = 2 * r.y + c.ltb;
     // A position whose queue is full (max_queue_len real columns) drops the event and
     // its time (connectivity/conv.py:57-99 truncates the queue).
     const bool act = NOTRUNC ? vc : (vc && st.y < c.mql);
@@ -335,7 +350,8 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
       }
     }
     const bool vcn = more && covers(rn, rn1);
-    const int2 stn = lds_ld_tc(vcn ? 2 * rn.y + c.ltb : c.tc_spare_b);
+    const int pabn = 2 * rn.y + c.ltb;
+    const int2 stn = lds_ld_tc(vcn ? pabn : c.tc_spare_b);
     uint64_t bal[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
@@ -353,12 +369,10 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
       // The spikes are the active lanes that did not keep their value: one compare.
       bal[it] = __ballot(true) & ~__ballot(keep);
     }
-    const bool mine = lane == e;
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       if (MODE == kStage) {
-        sg_lo[it] = mine ? (uint32_t)bal[it] : sg_lo[it];
-        sg_hi[it] = mine ? (uint32_t)(bal[it] >> 32) : sg_hi[it];
+        stage_to_lane(sg_lo[it], sg_hi[it], bal[it], e);
       } else if ((bal[it] >> lane) & 1) {
         // Bit = candidate index in the event's NC x NC grid (compaction decodes it).
         const size_t w = ((size_t)sk.b * sk.L + r1.y) * (size_t)(sk.OC * sk.WPO) +
@@ -370,6 +384,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     r1 = rn1;
     vc = vcn;
     st = stn;
+    pab = pabn;
     asm volatile("" ::: "memory");  // keep this event's LDS traffic before the next one's
   }
   if (MODE == kStage && lane < n_ev) {
