@@ -158,7 +158,7 @@ struct ConvLane {
   // byte offsets from the LDS base, for the event loop
   int extb;                     // decay table
   int lvb, lqb, ltb;            // register, code, (time, count) entry of an event's base
-  int v_spare_b, q_zero_b, tc_spare_b;
+  int v_spare_b, q_zero_b, tc_spare_b, tc_common_b;
   int GiVSb, GiQSb;             // per iteration
   int dmn, dmx, dth;            // register array -> extremes / per-neuron thresholds
 };
@@ -197,9 +197,12 @@ __device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, 
   c.lvb = b0 + (vw + c.lv) * 4;
   c.lqb = b0 + (qw + c.lq) * 4;
   c.ltb = b0 + tw * 4 + c.lp * 8;
+  // Lanes without a candidate in the event read one common spare (time, count) entry (a
+  // broadcast, not a bank conflict); their writes go to per-lane spare words.
   c.v_spare_b = b0 + (vw + c.v_spare) * 4;
   c.q_zero_b = b0 + (qw + c.q_zero) * 4;
   c.tc_spare_b = b0 + tw * 4 + c.tc_spare * 8;
+  c.tc_common_b = b0 + tw * 4 + PWs * 8;
   c.extb = (int)lds_addr(c.ext);
   c.GiVSb = c.GiVS * 4;
   c.GiQSb = c.GiQS * 4;
@@ -279,7 +282,8 @@ __device__ __forceinline__ void stage_to_lane(uint32_t& lo, uint32_t& hi, uint64
       "v_mov_b32 %[hi], %[vhi]\n\t"
       "s_mov_b64 exec, %[sv]"
       : [lo] "+v"(lo), [hi] "+v"(hi), [m] "=&s"(lane_mask), [sv] "=&s"(saved)
-      : [e] "s"(e), [vlo] "s"((uint32_t)v), [vhi] "s"((uint32_t)(v >> 32)));
+      : [e] "s"(e), [vlo] "s"((uint32_t)v), [vhi] "s"((uint32_t)(v >> 32))
+      : "scc");
 }
 
 // Where a wave's spikes go.
@@ -323,7 +327,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   int2 r1 = kRec1 ? c.rec1[0] : make_int2(0, 0);
   bool vc = covers(r, r1);
   int pab = 2 * r.y + c.ltb;  // this lane's (time, count) entry for the current event
-  int2 st = lds_ld_tc(vc ? pab : c.tc_spare_b);
+  int2 st = lds_ld_tc(vc ? pab : c.tc_common_b);
   for (int e = 0; e < n_ev; ++e) {
     const bool more = e + 1 < n_ev;
     const int en = more ? e + 1 : e;
@@ -351,7 +355,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     }
     const bool vcn = more && covers(rn, rn1);
     const int pabn = 2 * rn.y + c.ltb;
-    const int2 stn = lds_ld_tc(vcn ? pabn : c.tc_spare_b);
+    const int2 stn = lds_ld_tc(vcn ? pabn : c.tc_common_b);
     uint64_t bal[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
