@@ -526,17 +526,20 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   int vmin_l = 0, vmax_l = 0;
   int out_base = 0;  // spikes emitted so far (wave 0, merge mode)
 
-  // Next chunk of events, loaded one chunk ahead.
-  int t_n = 0, s_n = -1;
-  if (lane < n_eff) { t_n = time_ms(tb[lane]); s_n = sb_src[lane]; }
+  // Next chunk of events, loaded one chunk ahead and converted only when its chunk
+  // starts, so the loads' latency is covered by a chunk of work.  The index is clamped
+  // into the stream (entries past n_eff are not real: conv_decode checks j < n_eff).
+  float t_n = 0.0f;
+  int s_n = -1;
+  if (n_eff > 0) { t_n = tb[min(lane, n_eff - 1)]; s_n = sb_src[min(lane, n_eff - 1)]; }
 
   for (int base = 0; base < n_eff; base += kWave) {
     const int j = base + lane;
-    const int tv = t_n, sv = s_n;
+    const int tv = time_ms(t_n), sv = s_n;
     {
-      const int j2 = j + kWave;
-      t_n = 0; s_n = -1;
-      if (j2 < n_eff) { t_n = time_ms(tb[j2]); s_n = sb_src[j2]; }
+      const int j2 = min(j + kWave, n_eff - 1);
+      t_n = tb[j2];
+      s_n = sb_src[j2];
     }
     int oy0, ox0;
     const int n_ev = conv_decode(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0);

@@ -147,15 +147,19 @@ __global__ void __launch_bounds__(64) fc_layer_kernel(FcArgs a) {
   int t_prev = 0;  // the first event is compared with t = 0 (connectivity/fc.py:30)
   int out_base = 0;
 
-  int t_n = 0, s_n = 0;
-  if (lane < n_eff) { t_n = time_ms(tb[lane]); s_n = min(max(sb[lane], 0), a.n_in - 1); }
+  // The next chunk's events are loaded a chunk ahead and converted only when their
+  // chunk starts, so the loads' latency is covered by a chunk of work.
+  // Loads use an index clamped into the stream (entries past n_eff are never used).
+  float t_n = 0.0f;
+  int s_n = 0;
+  if (n_eff > 0) { t_n = tb[min(lane, n_eff - 1)]; s_n = sb[min(lane, n_eff - 1)]; }
 
   for (int base = 0; base < n_eff; base += kWave) {
-    const int tv = t_n, sv = s_n;
+    const int tv = time_ms(t_n), sv = min(max(s_n, 0), a.n_in - 1);
     {
-      const int j2 = base + kWave + lane;
-      t_n = 0; s_n = 0;
-      if (j2 < n_eff) { t_n = time_ms(tb[j2]); s_n = min(max(sb[j2], 0), a.n_in - 1); }
+      const int j2 = min(base + kWave + lane, n_eff - 1);
+      t_n = tb[j2];
+      s_n = sb[j2];
     }
     const int ne = min(kWave, n_eff - base);
     // Decay codes of the chunk's events (salt_core/quant/codes.py:87-105).
