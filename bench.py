@@ -56,6 +56,47 @@ def measured_traffic(kernel: str):
         return None
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def end_to_end(runner, w, dev, reps=5):
+    """Host -> device -> host: the events copied from pinned host memory, the whole network
+    in one salt_network_forward call, every layer's stream, registers and stats copied
+    back; the PCIe-inclusive time of one batch (median of reps)."""
+    import numpy as np
+    import torch
+    from salt_amd.stream import EventStream, unit_gain
+    t_h = torch.from_numpy(np.ascontiguousarray(w.events.event_times, dtype=np.float32)).pin_memory()
+    s_h = torch.from_numpy(np.ascontiguousarray(w.events.source_idx, dtype=np.int32)).pin_memory()
+    n_h = torch.from_numpy(np.ascontiguousarray(w.events.n_real_events, dtype=np.int32)).pin_memory()
+    outs_h = None
+    times = []
+    for _ in range(reps + 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        t_d = t_h.to(dev, non_blocking=True)
+        stream = EventStream(event_times=t_d, event_source_idx=s_h.to(dev, non_blocking=True),
+                             event_gain=unit_gain(t_d), n_real_events=n_h.to(dev, non_blocking=True))
+        outs = runner.run(stream)
+        if outs_h is None:
+            outs_h = [[torch.empty(x.shape, dtype=x.dtype, pin_memory=True)
+                       for x in (o.times, o.src, o.n, o.v_final, o.stats)] for o in outs]
+        for o, hs in zip(outs, outs_h):
+            for x, h in zip((o.times, o.src, o.n, o.v_final, o.stats), hs):
+                h.copy_(x, non_blocking=True)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times[1:])) * 1000.0
+
+
 def conv_update_counts(layer, src, n_real):
     """Per stream, the number of (neuron, event) register updates of a conv layer: the
     valid candidate positions of every real event x output channels (numpy, host)."""
@@ -133,6 +174,8 @@ def main() -> int:
     ms_per_step = wall * 1000.0 / args.steps
     value = n_events / (ms_per_step / 1000.0)
 
+    e2e_ms = end_to_end(runner, w, dev)
+
     # Algorithmic traffic of each layer (per launch): LDS = updates x (4 + 4 + weight bytes),
     # HBM = 8 B per input event + 8 B per spike + 4 B per final register + weights.
     host = [(o.src.cpu().numpy(), o.n.cpu().numpy()) for o in outs]
@@ -187,11 +230,20 @@ def main() -> int:
             ref = O.network_forward(specs, *w.events, nthreads=threads)
             runs.append(time.perf_counter() - t_c)
         cpu_s = float(np.median(runs))
+        # One thread on the first 64 streams (streams are independent and alike).
+        sub = tuple(np.ascontiguousarray(a[:64]) for a in w.events)
+        t_c = time.perf_counter()
+        O.network_forward(specs, *sub, nthreads=1)
+        one_s = time.perf_counter() - t_c
         cpu = {"value": round(n_events / cpu_s, 1), "unit": "input events/s", "cores": threads,
                "kind": "port",
                "sample": f"the full workload ({B} streams, {n_events} events, all three layers), "
                          f"oracle/salt_oracle.c -O3 with OpenMP over streams on {threads} host "
-                         f"threads; median of 3 runs, {cpu_s:.3f} s"}
+                         f"threads; median of 3 runs, {cpu_s:.3f} s",
+               "single_thread_value": round(int(sub[2].sum()) / one_s, 1),
+               "single_thread_sample": f"first 64 streams ({int(sub[2].sum())} events), 1 thread, "
+                                       f"{one_s:.3f} s",
+               "host_cpu": cpu_model()}
         bit_exact = True
         for o, r in zip(outs, ref):
             ok = (np.array_equal(o.n.cpu().numpy(), r["out_n"])
@@ -214,6 +266,11 @@ def main() -> int:
                    "round_mode": w.round_mode,
                    "f_a": 10, "f_V": 0, "i_V": 24, "overflow": "wrap"},
         "bit_exact": bit_exact, "fits": bool(fits.all()),
+        "end_to_end": {"ms": round(e2e_ms, 4), "value": round(n_events / (e2e_ms / 1000.0), 1),
+                       "unit": "input events/s",
+                       "what": "events from pinned host memory, one salt_network_forward call, "
+                               "every layer's stream, registers and stats back to pinned host "
+                               "memory (PCIe-inclusive), median of 5"},
         "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
