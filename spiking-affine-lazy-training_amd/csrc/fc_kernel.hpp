@@ -50,30 +50,17 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
   const int lane = threadIdx.x;
   // Lanes past the slice read a valid code of the slice (col is clamped) and are never
   // reported; their threshold is unreachable.
-  auto column = [&](int s, int k) -> int32_t {
-    return WLDS ? (int32_t)wl[s * sw + col[k]] : (int32_t)qt[(size_t)s * a.n_out + n0 + col[k]];
+  auto column = [&](int s, int k) -> QT {
+    return WLDS ? wl[s * sw + col[k]] : qt[(size_t)s * a.n_out + n0 + col[k]];
   };
-  int32_t qn[NPL];
-  {
-    const int s0 = rdlane(sv, 0);
-#pragma unroll
-    for (int k = 0; k < NPL; ++k) qn[k] = column(s0, k);
-  }
-  for (int e = 0; e < ne; ++e) {
-    int32_t qc[NPL];
-#pragma unroll
-    for (int k = 0; k < NPL; ++k) qc[k] = qn[k];
-    {
-      const int s1 = rdlane(sv, min(e + 1, kWave - 1));  // past the chunk: harmless reload
-#pragma unroll
-      for (int k = 0; k < NPL; ++k) qn[k] = column(s1, k);
-    }
+  // One event: process_event (salt_core/quant/scan.py:22-52) for every neuron, then its
+  // spikes (DIRECT: appended to the stream; else the chunk's spike-mask words).
+  auto step = [&](int e, const QT (&qc)[NPL]) {
     const int A = rdlane(Aj, e);
 #pragma unroll
     for (int k = 0; k < NPL; ++k) {
-      // process_event (salt_core/quant/scan.py:22-52).
       const int32_t d = decay_mul<F24>(V[k], A, fa, rc);
-      const int32_t u = (int32_t)((uint32_t)d + ((uint32_t)qc[k] << fV));
+      const int32_t u = (int32_t)((uint32_t)d + ((uint32_t)(int32_t)qc[k] << fV));
       const int32_t f = fit_bits<SAT>(u, qz);
       const bool fire = f >= vth[k];
       V[k] = fire ? 0 : f;
@@ -98,7 +85,25 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
               lane ? (uint32_t)(bal >> 32) : (uint32_t)bal;
       }
     }
+  };
+  auto load = [&](QT (&q)[NPL], int e) {  // past the chunk: a harmless reload
+    const int s_e = rdlane(sv, min(e, kWave - 1));
+#pragma unroll
+    for (int k = 0; k < NPL; ++k) q[k] = column(s_e, k);
+  };
+  // Two events per iteration with two column registers, each loaded one event before its
+  // use: the loads' latency is covered by an event of arithmetic and no register has to
+  // be copied or widened before its use (either would wait for the load).
+  QT qa[NPL], qb[NPL];
+  load(qa, 0);
+  int e = 0;
+  for (; e + 1 < ne; e += 2) {
+    load(qb, e + 1);
+    step(e, qa);
+    load(qa, e + 2);
+    step(e + 1, qb);
   }
+  if (e < ne) step(e, qa);
 }
 
 template <typename QT, int NPL, bool F24, bool SAT, bool WLDS>
