@@ -68,7 +68,7 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
       mx[k] = max(mx[k], u);
       const uint64_t bal = __ballot(fire);
       if (DIRECT) {
-        if (bal) {
+        if (__builtin_expect(bal != 0, 0)) {  // readout layers rarely fire
           if (fire) {
             const int idx = out_base + lanes_below(bal);
             if (idx < a.cap) {
