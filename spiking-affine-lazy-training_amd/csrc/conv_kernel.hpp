@@ -328,7 +328,8 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   bool vc = covers(r, r1);
   int pab = 2 * r.y + c.ltb;  // this lane's (time, count) entry for the current event
   int2 st = lds_ld_tc(vc ? pab : c.tc_common_b);
-  for (int e = 0; e < n_ev; ++e) {
+  // One event; (r, r1, vc, st, pab) become the next event's.
+  auto event = [&](int e) {
     const bool more = e + 1 < n_ev;
     const int en = more ? e + 1 : e;
     const int4 rn = c.rec[en];
@@ -390,7 +391,15 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     st = stn;
     pab = pabn;
     asm volatile("" ::: "memory");  // keep this event's LDS traffic before the next one's
+  };
+  // Two events per iteration: one loop branch per pair, and the carried state need not
+  // be copied between registers after every event.
+  int e = 0;
+  for (; e + 1 < n_ev; e += 2) {
+    event(e);
+    event(e + 1);
   }
+  if (e < n_ev) event(e);
   if (MODE == kStage && lane < n_ev) {
     const int jc = c.rec1[lane].y - base;  // the event's index within the chunk
 #pragma unroll
