@@ -88,7 +88,7 @@ __host__ __device__ inline int conv_tcn(int PWs) { return PWs + kWave; }
 __host__ __device__ inline int conv_wave_words(int Gp, int nit, int NC2, int PWs, bool stg,
                                                bool ext, bool vthn) {
   const int vs = conv_vs(PWs, NC2);
-  int w = kWave * 4 + kWave * 2 + (stg ? kWave * nit * 2 : 0) + 2 * conv_tcn(PWs) + Gp +
+  int w = (kWave + 1) * 6 + (stg ? kWave * nit * 2 : 0) + 2 * conv_tcn(PWs) + Gp +
           Gp * vs * (1 + (ext ? 2 : 0) + (vthn ? 1 : 0));
   return (w + 3) & ~3;
 }
@@ -118,8 +118,9 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int ncg, int nsb
   o = (o + 3) & ~3;
   l.shared_words = o;
   int w = 0;
-  l.rec = w;  w += kWave * 4;        // int4 {t, V base, weight base, candidate mask low}
-  l.rec1 = w; w += kWave * 2;        // int2 {candidate mask high, event index}
+  // One record more than a chunk's events: the sentinel after the last one.
+  l.rec = w;  w += (kWave + 1) * 4;  // int4 {t, V base, weight base, candidate mask low}
+  l.rec1 = w; w += (kWave + 1) * 2;  // int2 {candidate mask high, event index}
   l.stg = w;  w += kWave * nit * 2;  // uint64 spike ballot per (chunk event, iteration)
   l.tc = w;   w += 2 * l.tcn;        // int2 {last-update time, queue count}
   l.vthc = w; w += Gp;
@@ -233,8 +234,11 @@ __device__ __forceinline__ void lds_st_tc(int addr, int t, int cnt) {
 // Decodes the events of one chunk (connectivity/conv.py:15-43), one per lane (time tv,
 // source sv, index j; real when j < n_eff and sv >= 0), against the rows [r0, r0+rn):
 // records {time, position base * 4, code base * 4, candidate mask low} + {mask high,
-// event index} for the events with a candidate there, compacted in order.  Returns their
-// number; oy0/ox0 = the event's first candidate row and column.
+// event index} for the events with a candidate there, compacted in order, followed by
+// records with no candidate (mask 0) for the other lanes; with the permanent one at
+// index kWave, the record after a chunk's last event covers nothing, so the event loop
+// reads one record ahead without a bounds test.  Returns the number of events with a
+// candidate; oy0/ox0 = the event's first candidate row and column.
 __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c, int tv,
                                            int sv, int j, int n_eff, int r0, int rn, int& oy0,
                                            int& ox0) {
@@ -262,12 +266,11 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
   const int p0 = (oy0 - r0) * g.W + ox0;
   const int q0 = ch * g.K * g.K + (y + g.P - oy0 * g.S) * g.K + (x + g.P - ox0 * g.S);
   const uint64_t relm = __ballot(rel);
-  if (rel) {
-    const int slot = lanes_below(relm);
-    c.rec[slot] = make_int4(tv, p0 * 4, q0 * 4, (int)(uint32_t)m);
-    c.rec1[slot] = make_int2((int)(uint32_t)(m >> 32), j);
-  }
-  return __popcll(relm);
+  const int n = __popcll(relm);
+  const int slot = rel ? lanes_below(relm) : n + lanes_below(~relm);
+  c.rec[slot] = make_int4(tv, p0 * 4, q0 * 4, (int)(uint32_t)m);
+  c.rec1[slot] = make_int2((int)(uint32_t)(m >> 32), j);
+  return n;
 }
 
 // lo/hi of lane e <- the wave-uniform 64-bit value v; other lanes keep theirs.  Two
@@ -330,10 +333,8 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   int2 st = lds_ld_tc(vc ? pab : c.tc_common_b);
   // One event; (r, r1, vc, st, pab) become the next event's.
   auto event = [&](int e) {
-    const bool more = e + 1 < n_ev;
-    const int en = more ? e + 1 : e;
-    const int4 rn = c.rec[en];
-    const int2 rn1 = kRec1 ? c.rec1[en] : make_int2(0, 0);
+    const int4 rn = c.rec[e + 1];  // the sentinel after the last event covers nothing
+    const int2 rn1 = kRec1 ? c.rec1[e + 1] : make_int2(0, 0);
     // A position whose queue is full (max_queue_len real columns) drops the event and
     // its time (connectivity/conv.py:57-99 truncates the queue).
     const bool act = NOTRUNC ? vc : (vc && st.y < c.mql);
@@ -354,7 +355,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
         mxv[it] = lds_ld<int32_t>(va + it * c.GiVSb + c.dmx);
       }
     }
-    const bool vcn = more && covers(rn, rn1);
+    const bool vcn = covers(rn, rn1);
     const int pabn = 2 * rn.y + c.ltb;
     const int2 stn = lds_ld_tc(vcn ? pabn : c.tc_common_b);
     uint64_t bal[NIT];
@@ -517,6 +518,10 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
     }
   }
   for (int i = lane; i < lay.tcn; i += kWave) c.tc[i] = make_int2(0, 0);
+  if (lane == 0) {  // the record after a full chunk: no candidate
+    c.rec[kWave] = make_int4(0, 0, 0, 0);
+    c.rec1[kWave] = make_int2(0, 0);
+  }
   __syncthreads();
 
   conv_lane_setup(c, g, lane, Gi, VS, QS, PWs, oc0, qz.n_table, smem);
