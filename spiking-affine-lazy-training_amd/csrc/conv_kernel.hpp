@@ -14,9 +14,11 @@
 // candidate (dy, dx) = divmod(l % NC2, NC).  Relative to an event's first candidate
 // (oy0, ox0) = (ceil((y+P-K+1)/S), ceil((x+P-K+1)/S)) every address a lane needs is an
 // event-uniform base plus a lane constant:
-//   V slot    = ((oy0-r0)*W + ox0) + [slot*VS + dy*W + dx]
+//   V slot    = ((oy0-r0)*Wp + ox0) + [slot*VS + dy*Wp + dx]
 //   weight    = (c*K*K + (y+P-oy0*S)*K + (x+P-ox0*S)) + [slot*QS - dy*S*K - dx*S]
-// (VS, QS: odd per-slot strides).  Each wave decodes 64 events at a time (one per lane)
+// where Wp >= W is the row stride of the position arrays in LDS and VS, QS the slot
+// strides, chosen on the host so that a wave's accesses spread over the LDS banks
+// (the padding columns are never touched).  Each wave decodes 64 events at a time (one per lane)
 // into LDS records: those two bases, the time and a 64-bit mask of the candidates in
 // the output plane and its sub-band; the loop reads one record per event (a broadcast).
 //
@@ -42,11 +44,13 @@
 
 namespace salt {
 
-constexpr int kConvMaxWaves = 8;  // waves per work-group
+constexpr int kConvMaxWaves = 8;     // waves per stream (channel groups x sub-bands)
+constexpr int kConvBlockWaves = 16;  // waves per work-group (streams x waves per stream)
 
 // Geometry of a conv layer as the device code uses it.
 struct ConvGeom {
   int IC, Win, HWin, OC, K, S, P, H, W, HW, NC, NC2, mql;
+  int Wp;  // row stride of the per-position arrays in LDS (>= W)
 };
 
 struct ConvArgs {
@@ -55,6 +59,9 @@ struct ConvArgs {
   // partition: G channels per channel group in NIT iterations of Gi slots; ncg channel
   // groups x nsb sub-bands of Rw rows per work-group; R rows per work-group
   int G, Gi, ncg, nsb, Rw, R;
+  // spw streams per work-group (whole-plane plans), B streams in all
+  int spw, B;
+  int VS, QS;  // slot strides of the registers and the weight codes in LDS
   // quantisation
   Quant qz;
   const int32_t* table;
@@ -77,25 +84,13 @@ struct ConvArgs {
   uint32_t* masks;
 };
 
-// Odd slot strides with spare words, and the size of the per-position array.
-__host__ __device__ inline int conv_vs(int PWs, int NC2) { return (PWs + NC2) | 1; }
-__host__ __device__ inline int conv_qs(int ICKK) { return (ICKK + 1) | 1; }
+// Entries of the per-position (time, count) array: the band's PWs padded positions, then
+// one spare per lane.
 __host__ __device__ inline int conv_tcn(int PWs) { return PWs + kWave; }
-
-// LDS words of one wave's private state: records, staged ballots (nit per event when
-// stg), per-position (time, count), thresholds, registers and optional extremes /
-// per-neuron thresholds.  Codes are counted separately (shared, variable width).
-__host__ __device__ inline int conv_wave_words(int Gp, int nit, int NC2, int PWs, bool stg,
-                                               bool ext, bool vthn) {
-  const int vs = conv_vs(PWs, NC2);
-  int w = (kWave + 1) * 6 + (stg ? kWave * nit * 2 : 0) + 2 * conv_tcn(PWs) + Gp +
-          Gp * vs * (1 + (ext ? 2 : 0) + (vthn ? 1 : 0));
-  return (w + 3) & ~3;
-}
 
 // LDS layout of a conv_layer_kernel work-group, in 4-byte words: a shared part (decay
 // table, ballot-bit map, reduction slots, int32 weight codes per channel group), then
-// one region per wave.
+// one region per wave (spw streams x ncg x nsb waves).
 struct ConvLds {
   int ext, lanemap, red, qs, shared_words;                        // shared
   int rec, rec1, stg, tc, vthc, v, mn, mx, th, wave_words;        // per wave
@@ -103,17 +98,19 @@ struct ConvLds {
   int words;
 };
 
-__host__ __device__ inline ConvLds conv_lds_layout(int n_table, int ncg, int nsb, int Gp,
-                                                   int nit, int ICKK, int NC2, int PWs,
+// PWs: padded positions of a band (rows x Wp); vs >= PWs + NC2 and qs >= ICKK + 1: slot
+// strides (a slot's registers are followed by its NC2 spare words, its codes by a zero).
+__host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg, int nsb,
+                                                   int Gp, int nit, int vs, int qs, int PWs,
                                                    bool ext, bool vthn) {
   ConvLds l;
-  l.vs = conv_vs(PWs, NC2);
-  l.qst = conv_qs(ICKK);
+  l.vs = vs;
+  l.qst = qs;
   l.tcn = conv_tcn(PWs);
   int o = 0;
   l.ext = o;     o += n_table + 2;
   l.lanemap = o; o += 2 * kWave;  // int2 {slot, position offset} per ballot bit
-  l.red = o;     o += 4 * kConvMaxWaves;
+  l.red = o;     o += 4 * kConvBlockWaves;
   l.qs = o;      o += ncg * Gp * l.qst;
   o = (o + 3) & ~3;
   l.shared_words = o;
@@ -130,7 +127,7 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int ncg, int nsb
   l.th = w;   w += vthn ? Gp * l.vs : 0;
   w = (w + 3) & ~3;
   l.wave_words = w;
-  l.words = l.shared_words + ncg * nsb * w;
+  l.words = l.shared_words + spw * ncg * nsb * w;
   return l;
 }
 
@@ -181,7 +178,7 @@ __device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, 
   const int slot_t = lane_on ? slot0 : 0;
   c.lm = lane_on ? (1ull << c.cand) : 0ull;
   c.first = (lane_on && slot0 == 0) ? 1 : 0;
-  c.lp = dy * g.W + dx;
+  c.lp = dy * g.Wp + dx;
   c.lv = slot0 * VS + c.lp;
   c.lq = slot0 * QS - dy * g.S * g.K - dx * g.S;
   c.v_spare = slot_t * VS + PWs + c.cand;
@@ -263,7 +260,7 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
     const uint64_t cols = (2ull << dxB) - (1ull << dxA);
     for (int d = dyA; d <= dyB; ++d) m |= cols << (d * g.NC);
   }
-  const int p0 = (oy0 - r0) * g.W + ox0;
+  const int p0 = (oy0 - r0) * g.Wp + ox0;
   const int q0 = ch * g.K * g.K + (y + g.P - oy0 * g.S) * g.K + (x + g.P - ox0 * g.S);
   const uint64_t relm = __ballot(rel);
   const int n = __popcll(relm);
@@ -394,13 +391,28 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     asm volatile("" ::: "memory");  // keep this event's LDS traffic before the next one's
   };
   // Two events per iteration: one loop branch per pair, and the carried state need not
-  // be copied between registers after every event.
+  // be copied between registers after every event.  The wave's priority steps down from
+  // 3 to 0 over each quarter of the chunk: the waves of other streams sharing a SIMD are
+  // at other points of their chunks, so the one furthest behind in its own chunk is
+  // served first instead of the oldest wave, which would otherwise run ahead and leave
+  // the younger ones to finish alone, latency-bound, at the end of the kernel.
   int e = 0;
-  for (; e + 1 < n_ev; e += 2) {
-    event(e);
-    event(e + 1);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    switch (q) {
+      case 0: __builtin_amdgcn_s_setprio(3); break;
+      case 1: __builtin_amdgcn_s_setprio(2); break;
+      case 2: __builtin_amdgcn_s_setprio(1); break;
+      default: __builtin_amdgcn_s_setprio(0); break;
+    }
+    const int end = min(n_ev, (q + 1) * (kWave / 4));
+    for (; e + 1 < end; e += 2) {
+      event(e);
+      event(e + 1);
+    }
+    if (e < end) event(e++);
   }
-  if (e < n_ev) event(e);
+  __builtin_amdgcn_s_setprio(3);
   if (MODE == kStage && lane < n_ev) {
     const int jc = c.rec1[lane].y - base;  // the event's index within the chunk
 #pragma unroll
@@ -410,21 +422,24 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
 }
 
 // Catch-up column: decay to the last real input time T (connectivity/conv.py:102-125),
-// then the final registers of this wave's ocn channels over its PW positions.  An empty
-// position's catch-up has dt = 0; the identity columns after it repeat V.  A full queue
-// has no catch-up column.  Returns the largest per-position event count.
+// then the final registers of this wave's ocn channels over its PW positions (rows of W,
+// at row stride Wp in LDS).  An empty position's catch-up has dt = 0; the identity
+// columns after it repeat V.  A full queue has no catch-up column.  Returns the largest
+// per-position event count.
 template <bool F24, bool EXT>
 __device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane& c, int lane,
-                                           int T, int ocn, int PW, int VS, size_t v_base,
-                                           int HW, int32_t* v_final, int32_t* v_min,
-                                           int32_t* v_max, int& vmin_l, int& vmax_l) {
+                                           int T, int ocn, int PW, int W, int Wp, int VS,
+                                           size_t v_base, int HW, int32_t* v_final,
+                                           int32_t* v_min, int32_t* v_max, int& vmin_l,
+                                           int& vmax_l) {
   int maxcnt = 0;
-  for (int i = lane; i < PW; i += kWave) maxcnt = max(maxcnt, c.tc[i].y);
+  for (int i = lane; i < PW; i += kWave) maxcnt = max(maxcnt, c.tc[(i / W) * Wp + i % W].y);
   for (int li = lane; li < ocn * PW; li += kWave) {
     const int s = li / PW;
     const int p = li - s * PW;
-    const int2 st = c.tc[p];
-    const int vi = s * VS + p;
+    const int pp = (p / W) * Wp + p % W;  // the position in LDS
+    const int2 st = c.tc[pp];
+    const int vi = s * VS + pp;
     int32_t vv = c.Vs[vi];
     int32_t mnn = EXT ? c.mn[vi] : 0, mxx = EXT ? c.mx[vi] : 0;
     if (st.y < c.mql) {
@@ -446,26 +461,30 @@ __device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane& c, i
 }
 
 template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, bool M32, bool NOTRUNC>
-__global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvArgs a) {
+__global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(ConvArgs a) {
   extern __shared__ int32_t smem[];
   const ConvGeom& g = a.g;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int nthr = blockDim.x;
-  const int b = blockIdx.y;
-  const int cg = wv % a.ncg, sb = wv / a.ncg;  // channel group, sub-band
+  // Wave wv serves stream slot ks of the work-group's spw streams, as its wave wl.
+  const int nwps = a.ncg * a.nsb;
+  const int ks = wv / nwps, wl = wv - ks * nwps;
+  const int b = blockIdx.y * a.spw + ks;
+  const bool live = b < a.B;  // the last work-group's slots past the batch have no stream
+  const int cg = wl % a.ncg, sb = wl / a.ncg;  // channel group, sub-band
   const int Gi = a.Gi, Gp = NIT * a.Gi;
   const int oc0 = cg * a.G;
   const int ocn = max(0, min(a.G, g.OC - oc0));
   const int rows_end = min(g.H, (int)blockIdx.x * a.R + a.R);
   const int r0 = blockIdx.x * a.R + sb * a.Rw;
   const int rn = max(0, min(a.Rw, rows_end - r0));
-  const int W = g.W, PWs = a.Rw * W, PW = rn * W;
+  const int W = g.W, Wp = g.Wp, PWs = a.Rw * Wp, PW = rn * W;
   const int ICKK = g.IC * g.K * g.K;
   const Quant& qz = a.qz;
-  const ConvLds lay = conv_lds_layout(qz.n_table, a.ncg, a.nsb, Gp, NIT, ICKK, g.NC2, PWs,
-                                      EXT, VTHN);
+  const ConvLds lay = conv_lds_layout(qz.n_table, a.spw, a.ncg, a.nsb, Gp, NIT, a.VS, a.QS,
+                                      PWs, EXT, VTHN);
   const int VS = lay.vs, QS = lay.qst;
   int32_t* wbase = smem + lay.shared_words + wv * lay.wave_words;
   int2* lanemap = reinterpret_cast<int2*>(smem + lay.lanemap);
@@ -513,8 +532,10 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
     c.Vs[i] = 0;
     if (EXT) { c.mn[i] = 0; c.mx[i] = 0; }
     if (VTHN) {
-      const int s = i / VS, p = i - s * VS;
-      c.th[i] = (s < ocn && p < PW) ? qz.vth[(size_t)(oc0 + s) * g.HW + r0 * W + p] : INT_MAX;
+      const int s = i / VS, p = i - s * VS, row = p / Wp, col = p - row * Wp;
+      c.th[i] = (s < ocn && row < rn && col < W)
+                    ? qz.vth[(size_t)(oc0 + s) * g.HW + (r0 + row) * W + col]
+                    : INT_MAX;
     }
   }
   for (int i = lane; i < lay.tcn; i += kWave) c.tc[i] = make_int2(0, 0);
@@ -532,26 +553,36 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   sk.b = b; sk.masks = a.masks; sk.L = a.L; sk.OC = g.OC; sk.WPO = a.WPO; sk.Gi = Gi;
 
   const int L = a.L;
-  const int nr = a.n_real[b];
-  const int n_eff = nr < 0 ? 0 : (nr < L ? nr : L);
-  const float* tb = a.times + (size_t)b * L;
-  const int32_t* sb_src = a.src + (size_t)b * L;
+  auto real_count = [&](int bi) {
+    const int nr = bi < a.B ? a.n_real[bi] : 0;
+    return nr < 0 ? 0 : (nr < L ? nr : L);
+  };
+  const int n_eff = real_count(b);
+  // The chunk loop runs to the work-group's longest stream, so that every wave meets
+  // every barrier; a stream's chunks past its own events decode to no events.
+  int n_grp = 0;
+  for (int i = lane; i < a.spw; i += kWave) n_grp = max(n_grp, real_count(blockIdx.y * a.spw + i));
+  n_grp = __builtin_amdgcn_readfirstlane(wave_max(n_grp));
+  const float* tb = a.times + (size_t)(live ? b : 0) * L;
+  const int32_t* sb_src = a.src + (size_t)(live ? b : 0) * L;
 
   int vmin_l = 0, vmax_l = 0;
-  int out_base = 0;  // spikes emitted so far (wave 0, merge mode)
+  int out_base = 0;  // spikes emitted so far (the stream's first wave, merge mode)
 
   // Next chunk of events, loaded one chunk ahead and converted only when its chunk
   // starts, so the loads' latency is covered by a chunk of work.  The index is clamped
-  // into the stream (entries past n_eff are not real: conv_decode checks j < n_eff).
+  // into the stream (entries past n_eff are not real: conv_decode checks j < n_eff);
+  // a stream without events loads nothing.
+  const int jl = n_eff - 1;
   float t_n = 0.0f;
   int s_n = -1;
-  if (n_eff > 0) { t_n = tb[min(lane, n_eff - 1)]; s_n = sb_src[min(lane, n_eff - 1)]; }
+  if (jl >= 0) { t_n = tb[min(lane, jl)]; s_n = sb_src[min(lane, jl)]; }
 
-  for (int base = 0; base < n_eff; base += kWave) {
+  for (int base = 0; base < n_grp; base += kWave) {
     const int j = base + lane;
     const int tv = time_ms(t_n), sv = s_n;
-    {
-      const int j2 = min(j + kWave, n_eff - 1);
+    if (jl >= 0) {
+      const int j2 = min(j + kWave, jl);
       t_n = tb[j2];
       s_n = sb_src[j2];
     }
@@ -564,17 +595,17 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
       conv_events<NIT, F24, SAT, EXT, VTHN, kStage, M32, NOTRUNC>(qz, c, vtc, n_ev, base,
                                                                    sk, vmin_l, vmax_l);
       __syncthreads();  // every wave's ballots of this chunk are staged
-      if (wv == 0) {
-        // Walk (event, channel group, iteration, bit) = (event, ascending neuron id);
-        // the sub-bands' ballots of one event are disjoint and share the lane mapping.
-        const int nw = a.ncg * a.nsb;
+      if (wl == 0) {
+        // The stream's first wave walks (event, channel group, iteration, bit) = (event,
+        // ascending neuron id); the sub-bands' ballots of one event are disjoint and
+        // share the lane mapping.
+        const int32_t* stg0 = smem + lay.shared_words + ks * nwps * lay.wave_words + lay.stg;
         int cnt = 0;
         for (int gi = 0; gi < a.ncg; ++gi)
           for (int it = 0; it < NIT; ++it) {
             uint64_t bits = 0;
-            for (int w = gi; w < nw; w += a.ncg)
-              bits |= reinterpret_cast<const uint64_t*>(
-                  smem + lay.shared_words + w * lay.wave_words + lay.stg)[lane * NIT + it];
+            for (int w = gi; w < nwps; w += a.ncg)
+              bits |= reinterpret_cast<const uint64_t*>(stg0 + w * lay.wave_words)[lane * NIT + it];
             cnt += __popcll(bits);
           }
         const int excl = wave_excl_scan(cnt, lane);
@@ -586,9 +617,8 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
           for (int gi = 0; gi < a.ncg; ++gi)
             for (int it = 0; it < NIT; ++it) {
               uint64_t bits = 0;
-              for (int w = gi; w < nw; w += a.ncg)
-                bits |= reinterpret_cast<const uint64_t*>(
-                    smem + lay.shared_words + w * lay.wave_words + lay.stg)[lane * NIT + it];
+              for (int w = gi; w < nwps; w += a.ncg)
+                bits |= reinterpret_cast<const uint64_t*>(stg0 + w * lay.wave_words)[lane * NIT + it];
               while (bits) {
                 const int k = __builtin_ctzll(bits);
                 bits &= bits - 1;
@@ -613,9 +643,11 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
   }
 
   const int T = n_eff > 0 ? time_ms(tb[n_eff - 1]) : 0;
-  int maxcnt = conv_finish<F24, EXT>(qz, c, lane, T, ocn, PW, VS,
-                                     (size_t)b * (g.OC * g.HW) + (size_t)oc0 * g.HW + r0 * W,
-                                     g.HW, a.v_final, a.v_min, a.v_max, vmin_l, vmax_l);
+  int maxcnt = 0;
+  if (live)
+    maxcnt = conv_finish<F24, EXT>(qz, c, lane, T, ocn, PW, W, Wp, VS,
+                                   (size_t)b * (g.OC * g.HW) + (size_t)oc0 * g.HW + r0 * W,
+                                   g.HW, a.v_final, a.v_min, a.v_max, vmin_l, vmax_l);
   vmin_l = wave_min(vmin_l);
   vmax_l = wave_max(vmax_l);
   if (lane == 0) {
@@ -624,8 +656,8 @@ __global__ void __launch_bounds__(kWave * kConvMaxWaves) conv_layer_kernel(ConvA
     red[wv * 4 + 2] = maxcnt;
   }
   __syncthreads();
-  if (wv != 0) return;
-  for (int w = 1; w < a.ncg * a.nsb; ++w) {
+  if (wl != 0 || !live) return;
+  for (int w = wv + 1; w < wv + nwps; ++w) {  // the stream's other waves
     vmin_l = min(vmin_l, red[w * 4 + 0]);
     vmax_l = max(vmax_l, red[w * 4 + 1]);
     maxcnt = max(maxcnt, red[w * 4 + 2]);

@@ -15,10 +15,13 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
 
 #include "launch.hpp"
@@ -190,7 +193,8 @@ __global__ void transpose_kernel(const T* in, T* out, int n_out, int n_in) {
 // ------------------------------------------------------------------ planning
 
 struct ConvPlan {
-  int H, W, HW, NC, NC2, WPO, Gi, G, nit, ncg, nsb, Rw, R, n_rb, merge;
+  int H, W, HW, NC, NC2, WPO, Gi, G, nit, ncg, nsb, Rw, R, n_rb, merge, spw;
+  int Wp, VS, QS;  // LDS row stride and slot strides (choose_layout)
   size_t lds;
 };
 
@@ -201,10 +205,118 @@ int round_nit(int n) {  // smallest instantiated iteration count >= n
 
 size_t conv_lds_bytes(const salt_layer_desc* d, const salt_qparams* p, const ConvPlan& pl,
                       bool ext) {
-  const ConvLds l = conv_lds_layout(p->n_table, pl.ncg, pl.nsb, pl.nit * pl.Gi, pl.nit,
-                                    d->ic * d->k * d->k, pl.NC2, pl.Rw * pl.W, ext,
+  const ConvLds l = conv_lds_layout(p->n_table, pl.spw, pl.ncg, pl.nsb, pl.nit * pl.Gi, pl.nit,
+                                    pl.VS, pl.QS, pl.Rw * pl.Wp, ext,
                                     p->v_th_kind == SALT_VTH_PER_NEURON);
   return (size_t)l.words * 4;
+}
+
+// The plain layout: unpadded rows, the smallest odd slot strides.
+void default_layout(const salt_layer_desc* d, ConvPlan* pl) {
+  pl->Wp = pl->W;
+  pl->VS = (pl->Rw * pl->W + pl->NC2) | 1;
+  pl->QS = (d->ic * d->k * d->k + 1) | 1;
+}
+
+// Cycles one wave64 LDS access takes, as measured on gfx950: the two half-waves are
+// served one after the other, each by 32 banks (4-byte words for 32-bit accesses, 8-byte
+// words for 64-bit ones), and a half-wave takes as many cycles as the most distinct
+// addresses one bank holds (lanes on one address share it).  addr: word addresses,
+// -1 = lane without an access; unit: words per bank word (1 or 2).
+int lds_access_cycles(const int* addr, int unit) {
+  int total = 0;
+  for (int h = 0; h < kWave; h += 32) {
+    int seen[32][32], cnt[32] = {0}, worst = 0;
+    for (int l = h; l < h + 32; ++l) {
+      if (addr[l] < 0) continue;
+      const int u = addr[l] / unit, bank = u & 31;
+      bool dup = false;
+      for (int k = 0; k < cnt[bank] && !dup; ++k) dup = seen[bank][k] == u;
+      if (!dup) {
+        seen[bank][cnt[bank]++] = u;
+        worst = std::max(worst, cnt[bank]);
+      }
+    }
+    total += worst;
+  }
+  return total;
+}
+
+// Per-event LDS cycles of a wave's register, weight-code and (time, count) accesses,
+// averaged over the 32 bank alignments an event's base can take.  Lane l is slot l / NC2
+// (< Gi), candidate (dy, dx) = divmod(l % NC2, NC).
+enum ConvAccess { kAccV, kAccQ, kAccTC };
+double conv_access_cycles(ConvAccess which, int Gi, int NC, int S, int K, int Wp, int stride) {
+  const int NC2 = NC * NC;
+  int addr[kWave];
+  long sum = 0;
+  for (int base = 64; base < 96; ++base) {
+    for (int l = 0; l < kWave; ++l) {
+      const int slot = l / NC2, cand = l - slot * NC2, dy = cand / NC, dx = cand - dy * NC;
+      if (slot >= Gi) { addr[l] = -1; continue; }
+      switch (which) {
+        case kAccV: addr[l] = 4 * base + slot * stride + dy * Wp + dx; break;
+        case kAccQ: addr[l] = 4 * base + slot * stride - dy * S * K - dx * S; break;
+        default: addr[l] = 2 * (base + dy * Wp + dx); break;
+      }
+    }
+    sum += lds_access_cycles(addr, which == kAccTC ? 2 : 1);
+  }
+  return sum / 32.0;
+}
+
+// Chooses the row stride Wp >= W and the slot strides VS, QS of a plan that minimise the
+// modelled bank-conflict cycles of the event loop's LDS accesses (register read + write,
+// code read, (time, count) read + write; weights from the measured per-access costs),
+// within `budget` bytes of LDS per work-group.  Plans repeat for every call, so the
+// choice is cached.
+void choose_layout(const salt_layer_desc* d, const salt_qparams* p, bool ext, size_t budget,
+                   ConvPlan* pl) {
+  default_layout(d, pl);
+  const std::array<int, 16> key = {pl->W, pl->Rw, pl->Gi, pl->NC, d->s, d->k, d->ic, pl->nit,
+                                   pl->ncg, pl->nsb, pl->spw, p->n_table, (int)ext,
+                                   p->v_th_kind == SALT_VTH_PER_NEURON, (int)(budget >> 4),
+                                   (int)(budget & 15)};
+  static std::mutex mu;
+  static std::map<std::array<int, 16>, std::array<int, 3>> cache;
+  {
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) {
+      pl->Wp = it->second[0]; pl->VS = it->second[1]; pl->QS = it->second[2];
+      pl->lds = conv_lds_bytes(d, p, *pl, ext);
+      return;
+    }
+  }
+  const int ICKK = d->ic * d->k * d->k;
+  int best_qs = pl->QS;
+  double best_q = 1e30;
+  for (int qs = ICKK + 1; qs < ICKK + 1 + 64; ++qs) {
+    const double c = conv_access_cycles(kAccQ, pl->Gi, pl->NC, d->s, d->k, 0, qs);
+    if (c < best_q) { best_q = c; best_qs = qs; }
+  }
+  ConvPlan best = *pl;
+  double best_cost = 1e30;
+  for (int wp = pl->W; wp <= pl->W + 12; ++wp) {
+    const int pws = pl->Rw * wp;
+    int vs_best = 0;
+    double v_best = 1e30;
+    for (int vs = pws + pl->NC2; vs < pws + pl->NC2 + 64; ++vs) {
+      const double c = conv_access_cycles(kAccV, pl->Gi, pl->NC, d->s, d->k, wp, vs);
+      if (c < v_best) { v_best = c; vs_best = vs; }
+    }
+    ConvPlan t = *pl;
+    t.Wp = wp; t.VS = vs_best; t.QS = best_qs;
+    t.lds = conv_lds_bytes(d, p, t, ext);
+    if (t.lds > budget) continue;
+    const double tc = conv_access_cycles(kAccTC, pl->Gi, pl->NC, d->s, d->k, wp, 0);
+    const double cost = 3.2 * v_best + 4.3 * tc + 1.1 * best_q;
+    if (cost < best_cost - 1e-9) { best_cost = cost; best = t; }
+  }
+  if (best_cost < 1e29) *pl = best;
+  pl->lds = conv_lds_bytes(d, p, *pl, ext);
+  std::lock_guard<std::mutex> g(mu);
+  cache[key] = {pl->Wp, pl->VS, pl->QS};
 }
 
 // Fills the channel split of a plan: ncg channel groups of G channels, nit iterations
@@ -216,6 +328,7 @@ bool split_channels(int OC, int max_cg, ConvPlan* pl) {
     pl->ncg = ncg;
     pl->G = (OC + ncg - 1) / ncg;                       // balanced groups
     pl->nit = round_nit((pl->G + pl->Gi - 1) / pl->Gi);
+    pl->Gi = (pl->G + pl->nit - 1) / pl->nit;           // no more slots than channels
     return true;
   }
   return false;
@@ -255,14 +368,21 @@ int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool e
   nsb = std::max(1, std::min(nsb, kConvMaxWaves / pl->ncg));
   pl->Rw = (H + nsb - 1) / nsb;
   pl->nsb = (H + pl->Rw - 1) / pl->Rw;                // no empty sub-band
-  pl->R = H; pl->n_rb = 1; pl->merge = 1;
+  pl->R = H; pl->n_rb = 1; pl->merge = 1; pl->spw = 1;
+  default_layout(d, pl);
   pl->lds = conv_lds_bytes(d, p, *pl, ext);
-  if (pl->lds <= (size_t)kLdsMax) return 0;
+  if (pl->lds <= (size_t)kLdsMax) {
+    // padding may not cost a work-group per compute unit
+    const size_t per_cu = std::max<size_t>(1, (size_t)kLdsMax / pl->lds);
+    choose_layout(d, p, ext, (size_t)kLdsMax / per_cu, pl);
+    return 0;
+  }
   // Bands of rows, one work-group (of channel-group waves) each, within the budget.
   pl->nsb = 1; pl->merge = 0;
   int R = H;
   for (;;) {
     pl->Rw = pl->R = R;
+    default_layout(d, pl);
     pl->lds = conv_lds_bytes(d, p, *pl, ext);
     if (pl->lds <= (size_t)kLdsBandBudget || R == 1) break;
     --R;
@@ -270,7 +390,33 @@ int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool e
   if (pl->lds > (size_t)kLdsMax)
     return fail(-3, "conv: one output row does not fit in LDS (w_out=%d)", pl->W);
   pl->n_rb = (H + R - 1) / R;
+  choose_layout(d, p, ext, std::max(pl->lds, (size_t)kLdsBandBudget), pl);
   return 0;
+}
+
+// Streams per work-group of a whole-plane plan: one unless SALT_CONV_SPW=n asks for n
+// (within 16 waves and the LDS).  Several streams per work-group advance chunk by chunk
+// together, behind one barrier; on configuration 3 that was slower than independent
+// work-groups (the waves that finish a chunk first wait for the others), so it is a
+// tuning option, covered by the parity tests.
+void choose_spw(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext,
+                ConvPlan* pl) {
+  if (!pl->merge) return;
+  const int nwps = pl->ncg * pl->nsb;
+  const char* e = getenv("SALT_CONV_SPW");
+  int spw = e ? atoi(e) : 1;
+  if (spw <= 1) return;
+  spw = std::min({spw, kConvBlockWaves / nwps, std::max(B, 1)});
+  for (; spw > 1; --spw) {
+    ConvPlan t = *pl;
+    t.spw = spw;
+    const size_t lds = conv_lds_bytes(d, p, t, ext);
+    if (lds <= (size_t)kLdsMax) {
+      pl->spw = spw;
+      pl->lds = lds;
+      return;
+    }
+  }
 }
 
 struct FcPlan {
@@ -346,6 +492,7 @@ ConvGeom conv_geom(const salt_layer_desc* d, const ConvPlan& pl) {
   g.IC = d->ic; g.Win = d->w_in; g.HWin = d->h_in * d->w_in; g.OC = d->oc;
   g.K = d->k; g.S = d->s; g.P = d->p; g.H = pl.H; g.W = pl.W; g.HW = pl.HW;
   g.NC = pl.NC; g.NC2 = pl.NC2; g.mql = d->max_queue_len;
+  g.Wp = pl.Wp;
   return g;
 }
 
@@ -366,7 +513,7 @@ int32_t fill(int32_t* p, int32_t v, size_t n, hipStream_t st) {
 
 hipError_t launch_conv(const ConvArgs& a, const ConvPlan& pl, int flags, int B,
                        hipStream_t st) {
-  const dim3 grid(pl.n_rb, B), block(kWave * pl.ncg * pl.nsb);
+  const dim3 grid(pl.n_rb, (B + pl.spw - 1) / pl.spw), block(kWave * pl.ncg * pl.nsb * pl.spw);
   switch (pl.nit) {
 #define SALT_CASE(N) \
     case N: return launch_conv_nit##N(a, flags, grid, block, pl.lds, st);
@@ -412,10 +559,13 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     if (workspace_bytes < need || (need && !d_workspace))
       return fail(-1, "workspace of %zu bytes below the %zu needed", workspace_bytes, need);
     if (!launch) return 0;
+    choose_spw(desc, prm, B, ext, &pl);
     ConvArgs a;
     a.g = conv_geom(desc, pl);
     a.WPO = pl.WPO;
     a.G = pl.G; a.Gi = pl.Gi; a.ncg = pl.ncg; a.nsb = pl.nsb; a.Rw = pl.Rw; a.R = pl.R;
+    a.spw = pl.spw; a.B = B;
+    a.VS = pl.VS; a.QS = pl.QS;
     a.qz = qz; a.table = prm->d_decay_table; a.q = prm->d_q; a.q_bits = prm->q_bits;
     a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
     a.cap = out->cap; a.fill_pads = out->fill_pads; a.merge = pl.merge;

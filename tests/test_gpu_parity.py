@@ -104,6 +104,30 @@ def test_fc_matches_oracle(case, mi):
     assert_layer_equal(out, ref, tag=str(case))
 
 
+@pytest.mark.parametrize("spw", [2, 3, 4, 5])
+def test_conv_streams_per_work_group_match_oracle(spw, monkeypatch):
+    """Several streams per work-group (forced through SALT_CONV_SPW): streams of different
+    lengths, an empty one, and a last work-group with slots past the batch (B = 7, 11)
+    give the oracle's streams, registers and extremes."""
+    monkeypatch.setenv("SALT_CONV_SPW", str(spw))
+    for mi, case in enumerate([(2, 34, 34, 16, 5, 2, 0, 7, 400), (16, 15, 15, 32, 3, 2, 0, 11, 400),
+                               (2, 10, 10, 2, 3, 1, 0, 11, 200)]):
+        ic, h, w, oc, k, s, p, B, L = case
+        rng = np.random.default_rng(300 + 10 * spw + mi)
+        layer = ConvLayer(name="c", ic=ic, h_in=h, w_in=w, oc=oc, k=k, s=s, p=p, init_k=1.0,
+                          max_queue_len=int(rng.choice([L + 1, max(2, L // 20)])),
+                          max_out_spikes=int(rng.choice([4 * L * oc, 9])))
+        params, rm = _params(rng, layer.weight_shape, layer.n_neurons, oc, MODES[mi], 8,
+                             ["scalar", "channel", "neuron"][mi])
+        times, src, n_real = _events(rng, B, L, ic * h * w)
+        n_real[3] = L // 7  # a short stream beside full ones
+        print("spw", spw, "case", case, "n_real", n_real.tolist(), flush=True)
+        out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+        geom, prm, cap = oracle_spec(layer, params, rm)
+        ref = O.layer_forward(geom, prm, times, src, n_real, cap)
+        assert_layer_equal(out, ref, tag=f"spw {spw} {case}")
+
+
 def test_without_neuron_extremes_same_streams_and_registers():
     rng = np.random.default_rng(5)
     layer = ConvLayer(name="c", ic=2, h_in=34, w_in=34, oc=16, k=5, s=2, p=0, init_k=1.0,
