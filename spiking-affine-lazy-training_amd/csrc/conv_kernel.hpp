@@ -93,16 +93,18 @@ __host__ __device__ inline int conv_tcn(int PWs) { return PWs + kWave; }
 // one region per wave (spw streams x ncg x nsb waves).
 struct ConvLds {
   int ext, lanemap, red, qs, shared_words;                        // shared
-  int rec, rec1, stg, tc, vthc, v, mn, mx, th, wave_words;        // per wave
+  int rec, rec1, stg, tc, cnt, vthc, v, mn, mx, th, wave_words;   // per wave
   int vs, qst, tcn;
   int words;
 };
 
 // PWs: padded positions of a band (rows x Wp); vs >= PWs + NC2 and qs >= ICKK + 1: slot
 // strides (a slot's registers are followed by its NC2 spare words, its codes by a zero).
+// tsplit (no queue truncation possible): the per-position entries are last-update times
+// alone, and the queue counts a separate array (kept by the decode, read at the end).
 __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg, int nsb,
                                                    int Gp, int nit, int vs, int qs, int PWs,
-                                                   bool ext, bool vthn) {
+                                                   bool ext, bool vthn, bool tsplit) {
   ConvLds l;
   l.vs = vs;
   l.qst = qs;
@@ -119,7 +121,8 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg
   l.rec = w;  w += (kWave + 1) * 4;  // int4 {t, V base, weight base, candidate mask low}
   l.rec1 = w; w += (kWave + 1) * 2;  // int2 {candidate mask high, event index}
   l.stg = w;  w += kWave * nit * 2;  // uint64 spike ballot per (chunk event, iteration)
-  l.tc = w;   w += 2 * l.tcn;        // int2 {last-update time, queue count}
+  l.tc = w;   w += (tsplit ? 1 : 2) * l.tcn;  // {last-update time, queue count} or time
+  l.cnt = w;  w += tsplit ? PWs : 0;          // queue counts (tsplit)
   l.vthc = w; w += Gp;
   l.v = w;    w += Gp * l.vs;
   l.mn = w;   w += ext ? Gp * l.vs : 0;
@@ -147,6 +150,7 @@ struct ConvLane {
   int32_t* mn;
   int32_t* mx;
   int32_t* th;
+  int32_t* cnt;         // tsplit: queue counts of the band's positions
   uint64_t lm;          // this lane's candidate bit (0 for lanes without a slot)
   int first;            // slot 0: the lane that commits its position's time and count
   int lp, lv, lq;       // position / register / code offsets relative to an event's bases
@@ -167,10 +171,11 @@ __device__ __forceinline__ uint32_t lds_addr(const int32_t* p) {
 }
 
 // Lane constants for a wave of Gi slots per iteration over a band of PWs positions
-// (slot strides VS / QS), whose first channel is oc0.  base: the work-group's LDS.
+// (slot strides VS / QS), whose first channel is oc0; tcb: bytes per (time, count)
+// entry (8, or 4 for times alone).  base: the work-group's LDS.
 __device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, int lane,
                                                 int Gi, int VS, int QS, int PWs, int oc0,
-                                                int ntab, const int32_t* base) {
+                                                int ntab, int tcb, const int32_t* base) {
   const int slot0 = lane / g.NC2;
   c.cand = lane - slot0 * g.NC2;
   const int dy = c.cand / g.NC, dx = c.cand - (c.cand / g.NC) * g.NC;
@@ -194,13 +199,13 @@ __device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, 
   const int b0 = (int)lds_addr(base);
   c.lvb = b0 + (vw + c.lv) * 4;
   c.lqb = b0 + (qw + c.lq) * 4;
-  c.ltb = b0 + tw * 4 + c.lp * 8;
+  c.ltb = b0 + tw * 4 + c.lp * tcb;
   // Lanes without a candidate in the event read one common spare (time, count) entry (a
   // broadcast, not a bank conflict); their writes go to per-lane spare words.
   c.v_spare_b = b0 + (vw + c.v_spare) * 4;
   c.q_zero_b = b0 + (qw + c.q_zero) * 4;
-  c.tc_spare_b = b0 + tw * 4 + c.tc_spare * 8;
-  c.tc_common_b = b0 + tw * 4 + PWs * 8;
+  c.tc_spare_b = b0 + tw * 4 + c.tc_spare * tcb;
+  c.tc_common_b = b0 + tw * 4 + PWs * tcb;
   c.extb = (int)lds_addr(c.ext);
   c.GiVSb = c.GiVS * 4;
   c.GiQSb = c.GiQS * 4;
@@ -236,9 +241,11 @@ __device__ __forceinline__ void lds_st_tc(int addr, int t, int cnt) {
 // index kWave, the record after a chunk's last event covers nothing, so the event loop
 // reads one record ahead without a bounds test.  Returns the number of events with a
 // candidate; oy0/ox0 = the event's first candidate row and column.
+// cnt (queue counts of a wave that keeps them, else null): each event adds one to the
+// count of every candidate position it has.
 __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c, int tv,
                                            int sv, int j, int n_eff, int r0, int rn, int& oy0,
-                                           int& ox0) {
+                                           int& ox0, int32_t* cnt) {
   const bool real = j < n_eff && sv >= 0;
   int ch = 0, y = 0, x = 0;
   if (real) {
@@ -262,6 +269,9 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
   }
   const int p0 = (oy0 - r0) * g.Wp + ox0;
   const int q0 = ch * g.K * g.K + (y + g.P - oy0 * g.S) * g.K + (x + g.P - ox0 * g.S);
+  if (cnt && rel)
+    for (int d = dyA; d <= dyB; ++d)
+      for (int dx = dxA; dx <= dxB; ++dx) atomicAdd(&cnt[p0 + d * g.Wp + dx], 1);
   const uint64_t relm = __ballot(rel);
   const int n = __popcll(relm);
   const int slot = rel ? lanes_below(relm) : n + lanes_below(~relm);
@@ -323,11 +333,17 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   // Software pipeline: the record of event e+1 and its positions' (time, count) are
   // read while event e is processed (after e's own count/time write, so they are
   // current), which leaves one LDS round trip per event: decay code, registers, codes.
+  // NOTRUNC: the entries are last-update times alone (4 bytes; the decode keeps the
+  // queue counts), so st.y is unused.
+  auto tc_load = [&](int addr) -> int2 {
+    return NOTRUNC ? make_int2(lds_ld<int32_t>(addr), 0) : lds_ld_tc(addr);
+  };
+  constexpr int kTcShift = NOTRUNC ? 0 : 1;  // record position base (bytes of a word) -> entry
   int4 r = c.rec[0];
   int2 r1 = kRec1 ? c.rec1[0] : make_int2(0, 0);
   bool vc = covers(r, r1);
-  int pab = 2 * r.y + c.ltb;  // this lane's (time, count) entry for the current event
-  int2 st = lds_ld_tc(vc ? pab : c.tc_common_b);
+  int pab = (r.y << kTcShift) + c.ltb;  // this lane's (time, count) entry for the event
+  int2 st = tc_load(vc ? pab : c.tc_common_b);
   // One event; (r, r1, vc, st, pab) become the next event's.
   auto event = [&](int e) {
     const int4 rn = c.rec[e + 1];  // the sentinel after the last event covers nothing
@@ -335,8 +351,10 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     // A position whose queue is full (max_queue_len real columns) drops the event and
     // its time (connectivity/conv.py:57-99 truncates the queue).
     const bool act = NOTRUNC ? vc : (vc && st.y < c.mql);
-    lds_st_tc((vc && c.first) ? pab : c.tc_spare_b, NOTRUNC ? r.x : (act ? r.x : st.x),
-              st.y + 1);
+    if (NOTRUNC)
+      lds_st<int32_t>((vc && c.first) ? pab : c.tc_spare_b, r.x);
+    else
+      lds_st_tc((vc && c.first) ? pab : c.tc_spare_b, act ? r.x : st.x, st.y + 1);
     // Decay code: dt = 0 -> identity, 1..n -> table, > n -> 0 (an unsigned clamp).
     const int A = lds_ld<int32_t>(c.extb + (int)(min((uint32_t)(r.x - st.x), nt1) << 2));
     const int va = act ? r.y + c.lvb : c.v_spare_b;
@@ -353,8 +371,8 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
       }
     }
     const bool vcn = covers(rn, rn1);
-    const int pabn = 2 * rn.y + c.ltb;
-    const int2 stn = lds_ld_tc(vcn ? pabn : c.tc_common_b);
+    const int pabn = (rn.y << kTcShift) + c.ltb;
+    const int2 stn = tc_load(vcn ? pabn : c.tc_common_b);
     uint64_t bal[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
@@ -426,19 +444,23 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
 // at row stride Wp in LDS).  An empty position's catch-up has dt = 0; the identity
 // columns after it repeat V.  A full queue has no catch-up column.  Returns the largest
 // per-position event count.
-template <bool F24, bool EXT>
+template <bool F24, bool EXT, bool TSPLIT>
 __device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane& c, int lane,
                                            int T, int ocn, int PW, int W, int Wp, int VS,
                                            size_t v_base, int HW, int32_t* v_final,
                                            int32_t* v_min, int32_t* v_max, int& vmin_l,
                                            int& vmax_l) {
+  // (last-update time, queue count) of the position in LDS
+  auto entry = [&](int pp) -> int2 {
+    return TSPLIT ? make_int2(reinterpret_cast<const int32_t*>(c.tc)[pp], c.cnt[pp]) : c.tc[pp];
+  };
   int maxcnt = 0;
-  for (int i = lane; i < PW; i += kWave) maxcnt = max(maxcnt, c.tc[(i / W) * Wp + i % W].y);
+  for (int i = lane; i < PW; i += kWave) maxcnt = max(maxcnt, entry((i / W) * Wp + i % W).y);
   for (int li = lane; li < ocn * PW; li += kWave) {
     const int s = li / PW;
     const int p = li - s * PW;
     const int pp = (p / W) * Wp + p % W;  // the position in LDS
-    const int2 st = c.tc[pp];
+    const int2 st = entry(pp);
     const int vi = s * VS + pp;
     int32_t vv = c.Vs[vi];
     int32_t mnn = EXT ? c.mn[vi] : 0, mxx = EXT ? c.mx[vi] : 0;
@@ -484,7 +506,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int ICKK = g.IC * g.K * g.K;
   const Quant& qz = a.qz;
   const ConvLds lay = conv_lds_layout(qz.n_table, a.spw, a.ncg, a.nsb, Gp, NIT, a.VS, a.QS,
-                                      PWs, EXT, VTHN);
+                                      PWs, EXT, VTHN, NOTRUNC);
   const int VS = lay.vs, QS = lay.qst;
   int32_t* wbase = smem + lay.shared_words + wv * lay.wave_words;
   int2* lanemap = reinterpret_cast<int2*>(smem + lay.lanemap);
@@ -497,6 +519,9 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   c.rec1 = reinterpret_cast<int2*>(wbase + lay.rec1);
   c.stg = reinterpret_cast<uint64_t*>(wbase + lay.stg);
   c.tc = reinterpret_cast<int2*>(wbase + lay.tc);
+  // NOTRUNC: the queue counts of a (stream, sub-band) are kept by its first channel group
+  c.cnt = smem + lay.shared_words + (ks * nwps + sb * a.ncg) * lay.wave_words + lay.cnt;
+  int32_t* const cnt_kept = (NOTRUNC && cg == 0) ? c.cnt : nullptr;
   int32_t* vthc = wbase + lay.vthc;
   c.Vs = wbase + lay.v;
   c.mn = wbase + lay.mn;
@@ -538,14 +563,16 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
                     : INT_MAX;
     }
   }
-  for (int i = lane; i < lay.tcn; i += kWave) c.tc[i] = make_int2(0, 0);
+  for (int i = lane; i < (NOTRUNC ? 1 : 2) * lay.tcn; i += kWave) wbase[lay.tc + i] = 0;
+  if (NOTRUNC)
+    for (int i = lane; i < PWs; i += kWave) wbase[lay.cnt + i] = 0;
   if (lane == 0) {  // the record after a full chunk: no candidate
     c.rec[kWave] = make_int4(0, 0, 0, 0);
     c.rec1[kWave] = make_int2(0, 0);
   }
   __syncthreads();
 
-  conv_lane_setup(c, g, lane, Gi, VS, QS, PWs, oc0, qz.n_table, smem);
+  conv_lane_setup(c, g, lane, Gi, VS, QS, PWs, oc0, qz.n_table, NOTRUNC ? 4 : 8, smem);
   int vtc[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) vtc[it] = vthc[min(it * Gi + c.oc_lane - oc0, Gp - 1)];
@@ -587,7 +614,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
       s_n = sb_src[j2];
     }
     int oy0, ox0;
-    const int n_ev = conv_decode(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0);
+    const int n_ev = conv_decode(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0, cnt_kept);
     if (a.merge)
       for (int i = lane; i < kWave * NIT; i += kWave) c.stg[i] = 0;
     __syncthreads();
@@ -645,7 +672,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int T = n_eff > 0 ? time_ms(tb[n_eff - 1]) : 0;
   int maxcnt = 0;
   if (live)
-    maxcnt = conv_finish<F24, EXT>(qz, c, lane, T, ocn, PW, W, Wp, VS,
+    maxcnt = conv_finish<F24, EXT, NOTRUNC>(qz, c, lane, T, ocn, PW, W, Wp, VS,
                                    (size_t)b * (g.OC * g.HW) + (size_t)oc0 * g.HW + r0 * W,
                                    g.HW, a.v_final, a.v_min, a.v_max, vmin_l, vmax_l);
   vmin_l = wave_min(vmin_l);

@@ -195,6 +195,7 @@ __global__ void transpose_kernel(const T* in, T* out, int n_out, int n_in) {
 struct ConvPlan {
   int H, W, HW, NC, NC2, WPO, Gi, G, nit, ncg, nsb, Rw, R, n_rb, merge, spw;
   int Wp, VS, QS;  // LDS row stride and slot strides (choose_layout)
+  int tsplit;      // no queue truncation possible: times and counts in separate arrays
   size_t lds;
 };
 
@@ -207,7 +208,7 @@ size_t conv_lds_bytes(const salt_layer_desc* d, const salt_qparams* p, const Con
                       bool ext) {
   const ConvLds l = conv_lds_layout(p->n_table, pl.spw, pl.ncg, pl.nsb, pl.nit * pl.Gi, pl.nit,
                                     pl.VS, pl.QS, pl.Rw * pl.Wp, ext,
-                                    p->v_th_kind == SALT_VTH_PER_NEURON);
+                                    p->v_th_kind == SALT_VTH_PER_NEURON, pl.tsplit != 0);
   return (size_t)l.words * 4;
 }
 
@@ -273,12 +274,12 @@ double conv_access_cycles(ConvAccess which, int Gi, int NC, int S, int K, int Wp
 void choose_layout(const salt_layer_desc* d, const salt_qparams* p, bool ext, size_t budget,
                    ConvPlan* pl) {
   default_layout(d, pl);
-  const std::array<int, 16> key = {pl->W, pl->Rw, pl->Gi, pl->NC, d->s, d->k, d->ic, pl->nit,
+  const std::array<int, 17> key = {pl->W, pl->Rw, pl->Gi, pl->NC, d->s, d->k, d->ic, pl->nit,
                                    pl->ncg, pl->nsb, pl->spw, p->n_table, (int)ext,
-                                   p->v_th_kind == SALT_VTH_PER_NEURON, (int)(budget >> 4),
-                                   (int)(budget & 15)};
+                                   p->v_th_kind == SALT_VTH_PER_NEURON, pl->tsplit,
+                                   (int)(budget >> 4), (int)(budget & 15)};
   static std::mutex mu;
-  static std::map<std::array<int, 16>, std::array<int, 3>> cache;
+  static std::map<std::array<int, 17>, std::array<int, 3>> cache;
   {
     std::lock_guard<std::mutex> g(mu);
     auto it = cache.find(key);
@@ -347,8 +348,10 @@ bool plan_override(int* ncg_max, int* nsb) {
 // and channel groups see the same events, so they stay in step between the per-chunk
 // barriers; row sub-bands are supported but unbalanced for clustered events).
 // Otherwise several work-groups per stream each take a band of rows.
+// notrunc: max_queue_len >= the stream length, so no queue can be truncated.
 int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext,
-                  ConvPlan* pl) {
+                  bool notrunc, ConvPlan* pl) {
+  pl->tsplit = notrunc ? 1 : 0;
   pl->H = (d->h_in + 2 * d->p - d->k) / d->s + 1;
   pl->W = (d->w_in + 2 * d->p - d->k) / d->s + 1;
   if (pl->H < 1 || pl->W < 1) return fail(-1, "conv geometry gives an empty output plane");
@@ -553,7 +556,7 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
 
   if (desc->kind == SALT_LAYER_CONV) {
     ConvPlan pl;
-    rc = plan_conv(desc, prm, B, ext, &pl);
+    rc = plan_conv(desc, prm, B, ext, desc->max_queue_len >= L, &pl);
     if (rc) return rc;
     const size_t need = mask_bytes_conv(pl, desc, B, L);
     if (workspace_bytes < need || (need && !d_workspace))
@@ -580,7 +583,7 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     const int flags = (f24 ? kConvF24 : 0) | (sat ? kConvSat : 0) | (ext ? kConvExt : 0) |
                       (prm->v_th_kind == SALT_VTH_PER_NEURON ? kConvVthN : 0) |
                       (pl.NC2 <= 32 ? kConvM32 : 0) |
-                      (desc->max_queue_len >= L ? kConvNoTrunc : 0);
+                      (pl.tsplit ? kConvNoTrunc : 0);  // the layout follows this flag
     HIP_TRY(launch_conv(a, pl, flags, B, st));
     if (!pl.merge) {
       CompactArgs c;
@@ -707,7 +710,7 @@ int32_t salt_layer_workspace_size(const salt_layer_desc* desc, const salt_qparam
   if (!bytes || B < 0 || L < 0) return fail(-1, "invalid batch shape");
   if (desc->kind == SALT_LAYER_CONV) {
     ConvPlan pl;
-    rc = plan_conv(desc, prm, B, want_neuron_extremes != 0, &pl);
+    rc = plan_conv(desc, prm, B, want_neuron_extremes != 0, desc->max_queue_len >= L, &pl);
     if (rc) return rc;
     *bytes = mask_bytes_conv(pl, desc, B, L);
   } else {
@@ -743,7 +746,7 @@ int32_t salt_layer_trace(const salt_layer_desc* desc, const salt_qparams* prm,
   a.conv = conv;
   if (conv) {
     ConvPlan pl;
-    if ((rc = plan_conv(desc, prm, 1, false, &pl))) return rc;
+    if ((rc = plan_conv(desc, prm, 1, false, false, &pl))) return rc;
     a.IC = desc->ic; a.Hin = desc->h_in; a.Win = desc->w_in; a.K = desc->k; a.S = desc->s;
     a.P = desc->p; a.H = pl.H; a.W = pl.W; a.mql = desc->max_queue_len;
     a.n = desc->oc * pl.HW;
