@@ -3,11 +3,11 @@
 //
 // A work-group owns one stream and a band of R output rows (in-kernel output: the whole
 // plane).  Its waves split that band into ncg channel groups x nsb sub-bands of Rw rows;
-// every wave decodes all of the stream's events in order and processes those whose
-// candidate rows meet its sub-band.  Everything a wave touches per event lives in LDS:
-// registers V[channel slot][position], per-position (last-update time, queue count),
-// and -- shared by the waves of a channel group -- its weight codes and the extended
-// decay table.
+// each wave processes, in order, the stream's events whose candidate rows meet its
+// sub-band, as decoded by the sub-band's first channel group.  Everything a wave touches
+// per event lives in LDS: registers V[channel slot][position], per-position (last-update
+// time, queue count), and -- shared -- the weight codes of its channel group and the
+// extended decay table.
 //
 // Lane mapping.  NC = (k-1)//s + 1 candidate rows (and columns) per input event and
 // NC2 = NC*NC candidates; lane l is channel slot l / NC2 (+ Gi per iteration) and
@@ -18,9 +18,10 @@
 //   weight    = (c*K*K + (y+P-oy0*S)*K + (x+P-ox0*S)) + [slot*QS - dy*S*K - dx*S]
 // where Wp >= W is the row stride of the position arrays in LDS and VS, QS the slot
 // strides, chosen on the host so that a wave's accesses spread over the LDS banks
-// (the padding columns are never touched).  Each wave decodes 64 events at a time (one per lane)
-// into LDS records: those two bases, the time and a 64-bit mask of the candidates in
-// the output plane and its sub-band; the loop reads one record per event (a broadcast).
+// (the padding columns are never touched).  The decoding wave turns 64 events at a time
+// (one per lane) into LDS records: those two bases, the time and a 64-bit mask of the
+// candidates in the output plane and its sub-band; the loop reads one record per event
+// (a broadcast).
 //
 // No lane predicates in the event loop.  A lane without an update this event (no
 // candidate, or a full queue) reads and writes its own spare words, which hold zeros:
@@ -515,13 +516,18 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   ConvLane c;
   c.ext = ext;
   c.qs = smem + lay.qs + cg * Gp * QS;
-  c.rec = reinterpret_cast<int4*>(wbase + lay.rec);
-  c.rec1 = reinterpret_cast<int2*>(wbase + lay.rec1);
+  // The first channel group of a (stream, sub-band) decodes its events (and, NOTRUNC,
+  // keeps the queue counts); the other channel groups see the same events and read its
+  // records.
+  const bool dec = cg == 0;
+  const int dw = ks * nwps + sb * a.ncg;  // the decoding wave
+  int32_t* const dbase = smem + lay.shared_words + dw * lay.wave_words;
+  c.rec = reinterpret_cast<int4*>(dbase + lay.rec);
+  c.rec1 = reinterpret_cast<int2*>(dbase + lay.rec1);
   c.stg = reinterpret_cast<uint64_t*>(wbase + lay.stg);
   c.tc = reinterpret_cast<int2*>(wbase + lay.tc);
-  // NOTRUNC: the queue counts of a (stream, sub-band) are kept by its first channel group
-  c.cnt = smem + lay.shared_words + (ks * nwps + sb * a.ncg) * lay.wave_words + lay.cnt;
-  int32_t* const cnt_kept = (NOTRUNC && cg == 0) ? c.cnt : nullptr;
+  c.cnt = dbase + lay.cnt;
+  int32_t* const cnt_kept = (NOTRUNC && dec) ? c.cnt : nullptr;
   int32_t* vthc = wbase + lay.vthc;
   c.Vs = wbase + lay.v;
   c.mn = wbase + lay.mn;
@@ -566,7 +572,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   for (int i = lane; i < (NOTRUNC ? 1 : 2) * lay.tcn; i += kWave) wbase[lay.tc + i] = 0;
   if (NOTRUNC)
     for (int i = lane; i < PWs; i += kWave) wbase[lay.cnt + i] = 0;
-  if (lane == 0) {  // the record after a full chunk: no candidate
+  if (dec && lane == 0) {  // the record after a full chunk: no candidate
     c.rec[kWave] = make_int4(0, 0, 0, 0);
     c.rec1[kWave] = make_int2(0, 0);
   }
@@ -603,21 +609,25 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int jl = n_eff - 1;
   float t_n = 0.0f;
   int s_n = -1;
-  if (jl >= 0) { t_n = tb[min(lane, jl)]; s_n = sb_src[min(lane, jl)]; }
+  if (dec && jl >= 0) { t_n = tb[min(lane, jl)]; s_n = sb_src[min(lane, jl)]; }
 
   for (int base = 0; base < n_grp; base += kWave) {
     const int j = base + lane;
     const int tv = time_ms(t_n), sv = s_n;
-    if (jl >= 0) {
-      const int j2 = min(j + kWave, jl);
-      t_n = tb[j2];
-      s_n = sb_src[j2];
+    int oy0 = 0, ox0 = 0, n_ev = 0;
+    if (dec) {
+      if (jl >= 0) {
+        const int j2 = min(j + kWave, jl);
+        t_n = tb[j2];
+        s_n = sb_src[j2];
+      }
+      n_ev = conv_decode(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0, cnt_kept);
+      if (lane == 0) red[dw * 4 + 3] = n_ev;
     }
-    int oy0, ox0;
-    const int n_ev = conv_decode(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0, cnt_kept);
     if (a.merge)
       for (int i = lane; i < kWave * NIT; i += kWave) c.stg[i] = 0;
     __syncthreads();
+    if (!dec) n_ev = __builtin_amdgcn_readfirstlane(red[dw * 4 + 3]);
     if (a.merge) {
       conv_events<NIT, F24, SAT, EXT, VTHN, kStage, M32, NOTRUNC>(qz, c, vtc, n_ev, base,
                                                                    sk, vmin_l, vmax_l);
