@@ -53,9 +53,15 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
   auto column = [&](int s, int k) -> QT {
     return WLDS ? wl[s * sw + col[k]] : qt[(size_t)s * a.n_out + n0 + col[k]];
   };
+  // DIRECT: bit e & 31 of fired[h][k] (h = e / 32) records that this lane's neuron k
+  // fired at the chunk's event e -- vector operations only, so that the event loop has
+  // no branch on the compare -- and the chunk's spikes are appended after its events.
+  uint32_t fired[2][NPL];
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) fired[0][k] = fired[1][k] = 0;
   // One event: process_event (salt_core/quant/scan.py:22-52) for every neuron, then its
-  // spikes (DIRECT: appended to the stream; else the chunk's spike-mask words).
-  auto step = [&](int e, const QT (&qc)[NPL]) {
+  // spikes (DIRECT: recorded in fired[h]; else the chunk's spike-mask words).
+  auto step = [&](int e, const QT (&qc)[NPL], uint32_t (&fh)[NPL]) {
     const int A = rdlane(Aj, e);
 #pragma unroll
     for (int k = 0; k < NPL; ++k) {
@@ -66,19 +72,10 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
       V[k] = fire ? 0 : f;
       mn[k] = min(mn[k], u);
       mx[k] = max(mx[k], u);
-      const uint64_t bal = __ballot(fire);
       if (DIRECT) {
-        if (__builtin_expect(bal != 0, 0)) {  // readout layers rarely fire
-          if (fire) {
-            const int idx = out_base + lanes_below(bal);
-            if (idx < a.cap) {
-              a.out_t[(size_t)b * a.cap + idx] = (float)rdlane(tv, e);
-              a.out_s[(size_t)b * a.cap + idx] = n0 + k * kWave + lane;
-            }
-          }
-          out_base += __popcll(bal);
-        }
+        fh[k] |= fire ? (1u << (e & 31)) : 0u;
       } else {
+        const uint64_t bal = __ballot(fire);
         const int w0 = (n0 + k * kWave) >> 5;
         if (lane < 2 && w0 + lane < a.words)
           a.masks[((size_t)b * a.L + base + e) * a.words + w0 + lane] =
@@ -97,13 +94,46 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
   QT qa[NPL], qb[NPL];
   load(qa, 0);
   int e = 0;
-  for (; e + 1 < ne; e += 2) {
-    load(qb, e + 1);
-    step(e, qa);
-    load(qa, e + 2);
-    step(e + 1, qb);
+  // events [e, end) recording into fh; end is even unless it is ne
+  auto run = [&](int end, uint32_t (&fh)[NPL]) {
+    for (; e + 1 < end; e += 2) {
+      load(qb, e + 1);
+      step(e, qa, fh);
+      load(qa, e + 2);
+      step(e + 1, qb, fh);
+    }
+    if (e < end) step(e++, qa, fh);
+  };
+  run(min(ne, 32), fired[0]);
+  run(ne, fired[1]);
+  if (DIRECT) {
+    uint32_t any = 0;
+#pragma unroll
+    for (int k = 0; k < NPL; ++k) any |= fired[0][k] | fired[1][k];
+    if (__builtin_expect(__ballot(any != 0) != 0, 0)) {  // readout layers rarely fire
+      // (event, neuron) order: per event, the slice's neurons in ascending order
+      for (int e2 = 0; e2 < ne; ++e2) {
+        const int h = e2 >> 5, sh = e2 & 31;
+        // read with every lane active: a lane's VGPR value is only kept for the lanes
+        // that use it, so a read of another lane inside the branch below may see a reuse
+        const float te = (float)rdlane(tv, e2);
+#pragma unroll
+        for (int k = 0; k < NPL; ++k) {
+          const bool f = ((h ? fired[1][k] : fired[0][k]) >> sh) & 1u;
+          const uint64_t bal = __ballot(f);
+          if (bal == 0) continue;
+          if (f) {
+            const int idx = out_base + lanes_below(bal);
+            if (idx < a.cap) {
+              a.out_t[(size_t)b * a.cap + idx] = te;
+              a.out_s[(size_t)b * a.cap + idx] = n0 + k * kWave + lane;
+            }
+          }
+          out_base += __popcll(bal);
+        }
+      }
+    }
   }
-  if (e < ne) step(e, qa);
 }
 
 template <typename QT, int NPL, bool F24, bool SAT, bool WLDS>
