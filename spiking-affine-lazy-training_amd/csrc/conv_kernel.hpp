@@ -118,9 +118,9 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg
   o = (o + 3) & ~3;
   l.shared_words = o;
   int w = 0;
-  // One record more than a chunk's events: the sentinel after the last one.
-  l.rec = w;  w += (kWave + 1) * 4;  // int4 {t, V base, weight base, candidate mask low}
-  l.rec1 = w; w += (kWave + 1) * 2;  // int2 {candidate mask high, event index}
+  // Two records more than a chunk's events: the loop reads two records ahead.
+  l.rec = w;  w += (kWave + 2) * 4;  // int4 {t, V base, weight base, candidate mask low}
+  l.rec1 = w; w += (kWave + 2) * 2;  // int2 {candidate mask high, event index}
   l.stg = w;  w += kWave * nit * 2;  // uint64 spike ballot per (chunk event, iteration)
   l.tc = w;   w += (tsplit ? 1 : 2) * l.tcn;  // {last-update time, queue count} or time
   l.cnt = w;  w += tsplit ? PWs : 0;          // queue counts (tsplit)
@@ -153,7 +153,6 @@ struct ConvLane {
   int32_t* th;
   int32_t* cnt;         // tsplit: queue counts of the band's positions
   uint64_t lm;          // this lane's candidate bit (0 for lanes without a slot)
-  int first;            // slot 0: the lane that commits its position's time and count
   int lp, lv, lq;       // position / register / code offsets relative to an event's bases
   int v_spare, q_zero, tc_spare;  // this lane's spare register word, zero code, spare entry
   int GiVS, GiQS;
@@ -183,7 +182,6 @@ __device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, 
   const bool lane_on = slot0 < Gi;
   const int slot_t = lane_on ? slot0 : 0;
   c.lm = lane_on ? (1ull << c.cand) : 0ull;
-  c.first = (lane_on && slot0 == 0) ? 1 : 0;
   c.lp = dy * g.Wp + dx;
   c.lv = slot0 * VS + c.lp;
   c.lq = slot0 * QS - dy * g.S * g.K - dx * g.S;
@@ -331,66 +329,85 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     if (M32) return ((uint32_t)r.w & lm32) != 0u;
     return ((((uint64_t)(uint32_t)r1.x << 32) | (uint32_t)r.w) & c.lm) != 0;
   };
-  // Software pipeline: the record of event e+1 and its positions' (time, count) are
-  // read while event e is processed (after e's own count/time write, so they are
-  // current), which leaves one LDS round trip per event: decay code, registers, codes.
-  // NOTRUNC: the entries are last-update times alone (4 bytes; the decode keeps the
-  // queue counts), so st.y is unused.
+  // Software pipeline over two events.  LDS completes a wave's operations in order, so
+  // a read issued after a write sees it: event e+1's registers, codes and decay code are
+  // read right after event e has written its registers, and are waited for only when e+1
+  // is updated -- one LDS round trip per event on the register chain.  Meanwhile event e
+  // writes its positions' times, reads e+1's (after that write, so they are current) and
+  // fetches the record of e+2.  NOTRUNC: the entries are last-update times alone (4 bytes;
+  // the decode keeps the queue counts), so st.y is unused.
   auto tc_load = [&](int addr) -> int2 {
     return NOTRUNC ? make_int2(lds_ld<int32_t>(addr), 0) : lds_ld_tc(addr);
   };
   constexpr int kTcShift = NOTRUNC ? 0 : 1;  // record position base (bytes of a word) -> entry
+  // An event's operands: register / code addresses and the values read there.
+  struct Ops {
+    int va, qa, A;
+    int v[NIT], qv[NIT], vt[NIT], mnv[NIT], mxv[NIT];
+  };
+  // A position whose queue is full (max_queue_len real columns) drops the event and
+  // its time (connectivity/conv.py:57-99 truncates the queue).
+  auto act_of = [&](bool vc, const int2& st) { return NOTRUNC ? vc : (vc && st.y < c.mql); };
+  auto read_ops = [&](Ops& o, const int4& r, bool vc, const int2& st) {
+    const bool act = act_of(vc, st);
+    // Decay code: dt = 0 -> identity, 1..n -> table, > n -> 0 (an unsigned clamp).
+    o.A = lds_ld<int32_t>(c.extb + (int)(min((uint32_t)(r.x - st.x), nt1) << 2));
+    o.va = act ? r.y + c.lvb : c.v_spare_b;
+    o.qa = act ? r.z + c.lqb : c.q_zero_b;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      o.v[it] = lds_ld<int32_t>(o.va + it * c.GiVSb);
+      o.qv[it] = lds_ld<int32_t>(o.qa + it * c.GiQSb);
+      o.vt[it] = VTHN ? lds_ld<int32_t>(o.va + it * c.GiVSb + c.dth) : vtc[it];
+      if (EXT) {
+        o.mnv[it] = lds_ld<int32_t>(o.va + it * c.GiVSb + c.dmn);
+        o.mxv[it] = lds_ld<int32_t>(o.va + it * c.GiVSb + c.dmx);
+      }
+    }
+  };
   int4 r = c.rec[0];
   int2 r1 = kRec1 ? c.rec1[0] : make_int2(0, 0);
   bool vc = covers(r, r1);
   int pab = (r.y << kTcShift) + c.ltb;  // this lane's (time, count) entry for the event
   int2 st = tc_load(vc ? pab : c.tc_common_b);
-  // One event; (r, r1, vc, st, pab) become the next event's.
+  int4 rn = c.rec[1];  // records past the last event cover nothing
+  int2 rn1 = kRec1 ? c.rec1[1] : make_int2(0, 0);
+  Ops o;
+  read_ops(o, r, vc, st);
+  // One event; everything carried becomes the next event's.
   auto event = [&](int e) {
-    const int4 rn = c.rec[e + 1];  // the sentinel after the last event covers nothing
-    const int2 rn1 = kRec1 ? c.rec1[e + 1] : make_int2(0, 0);
-    // A position whose queue is full (max_queue_len real columns) drops the event and
-    // its time (connectivity/conv.py:57-99 truncates the queue).
-    const bool act = NOTRUNC ? vc : (vc && st.y < c.mql);
+    // this event's positions: time (and count), written by every lane of the position
+    // (the slots of one candidate write the same entry with the same value)
     if (NOTRUNC)
-      lds_st<int32_t>((vc && c.first) ? pab : c.tc_spare_b, r.x);
+      lds_st<int32_t>(vc ? pab : c.tc_spare_b, r.x);
     else
-      lds_st_tc((vc && c.first) ? pab : c.tc_spare_b, act ? r.x : st.x, st.y + 1);
-    // Decay code: dt = 0 -> identity, 1..n -> table, > n -> 0 (an unsigned clamp).
-    const int A = lds_ld<int32_t>(c.extb + (int)(min((uint32_t)(r.x - st.x), nt1) << 2));
-    const int va = act ? r.y + c.lvb : c.v_spare_b;
-    const int qa = act ? r.z + c.lqb : c.q_zero_b;
-    int v[NIT], qv[NIT], vt[NIT], mnv[NIT], mxv[NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      v[it] = lds_ld<int32_t>(va + it * c.GiVSb);
-      qv[it] = lds_ld<int32_t>(qa + it * c.GiQSb);
-      vt[it] = VTHN ? lds_ld<int32_t>(va + it * c.GiVSb + c.dth) : vtc[it];
-      if (EXT) {
-        mnv[it] = lds_ld<int32_t>(va + it * c.GiVSb + c.dmn);
-        mxv[it] = lds_ld<int32_t>(va + it * c.GiVSb + c.dmx);
-      }
-    }
+      lds_st_tc(vc ? pab : c.tc_spare_b, act_of(vc, st) ? r.x : st.x, st.y + 1);
+    // the next event's positions, after that write
     const bool vcn = covers(rn, rn1);
     const int pabn = (rn.y << kTcShift) + c.ltb;
     const int2 stn = tc_load(vcn ? pabn : c.tc_common_b);
+    const int4 rn2 = c.rec[e + 2];
+    const int2 rn12 = kRec1 ? c.rec1[e + 2] : make_int2(0, 0);
+    asm volatile("" ::: "memory");  // the reads above go out before this event's update
     uint64_t bal[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-      const int32_t d = decay_mul<F24>(v[it], A, fa, rc);
-      const int32_t u = (int32_t)((uint32_t)d + (uint32_t)qv[it]);  // codes hold q*2^f_V
+      const int32_t d = decay_mul<F24>(o.v[it], o.A, fa, rc);
+      const int32_t u = (int32_t)((uint32_t)d + (uint32_t)o.qv[it]);  // codes hold q*2^f_V
       const int32_t f = fit_bits<SAT>(u, qz);
-      const bool keep = f < vt[it];
-      lds_st<int32_t>(va + it * c.GiVSb, keep ? f : 0);
+      const bool keep = f < o.vt[it];
+      lds_st<int32_t>(o.va + it * c.GiVSb, keep ? f : 0);
       vmin_l = min(vmin_l, u);
       vmax_l = max(vmax_l, u);
       if (EXT) {
-        lds_st<int32_t>(va + it * c.GiVSb + c.dmn, min(mnv[it], u));
-        lds_st<int32_t>(va + it * c.GiVSb + c.dmx, max(mxv[it], u));
+        lds_st<int32_t>(o.va + it * c.GiVSb + c.dmn, min(o.mnv[it], u));
+        lds_st<int32_t>(o.va + it * c.GiVSb + c.dmx, max(o.mxv[it], u));
       }
       // The spikes are the active lanes that did not keep their value: one compare.
       bal[it] = __ballot(true) & ~__ballot(keep);
     }
+    asm volatile("" ::: "memory");  // the next event's reads come after these writes
+    read_ops(o, rn, vcn, stn);
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       if (MODE == kStage) {
@@ -407,7 +424,8 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     vc = vcn;
     st = stn;
     pab = pabn;
-    asm volatile("" ::: "memory");  // keep this event's LDS traffic before the next one's
+    rn = rn2;
+    rn1 = rn12;
   };
   // Two events per iteration: one loop branch per pair, and the carried state need not
   // be copied between registers after every event.  The wave's priority steps down from
@@ -572,9 +590,9 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   for (int i = lane; i < (NOTRUNC ? 1 : 2) * lay.tcn; i += kWave) wbase[lay.tc + i] = 0;
   if (NOTRUNC)
     for (int i = lane; i < PWs; i += kWave) wbase[lay.cnt + i] = 0;
-  if (dec && lane == 0) {  // the record after a full chunk: no candidate
-    c.rec[kWave] = make_int4(0, 0, 0, 0);
-    c.rec1[kWave] = make_int2(0, 0);
+  if (dec && lane < 2) {  // the records after a full chunk: no candidate
+    c.rec[kWave + lane] = make_int4(0, 0, 0, 0);
+    c.rec1[kWave + lane] = make_int2(0, 0);
   }
   __syncthreads();
 
