@@ -13,11 +13,11 @@ namespace {
 
 template <int NIT, int F>
 hipError_t conv_entry(const ConvArgs& a, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
-  constexpr bool kF24 = (F & kConvF24) != 0, kSat = (F & kConvSat) != 0,
+  constexpr bool kSat = (F & kConvSat) != 0,
                  kExt = (F & kConvExt) != 0, kVthN = (F & kConvVthN) != 0,
                  kM32 = (F & kConvM32) != 0, kNoTrunc = (F & kConvNoTrunc) != 0;
   static bool attr_set = false;
-  auto fn = conv_layer_kernel<NIT, kF24, kSat, kExt, kVthN, kM32, kNoTrunc>;
+  auto fn = conv_layer_kernel<NIT, kSat, kExt, kVthN, kM32, kNoTrunc>;
   return launch_with_lds(reinterpret_cast<const void*>(fn), fn, &attr_set, grid, block, lds, st,
                          a);
 }

@@ -279,20 +279,18 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
   return n;
 }
 
-// lo/hi of lane e <- the wave-uniform 64-bit value v; other lanes keep theirs.  Two
-// moves under a one-lane exec mask (saved and restored inside the block), which is
-// fewer vector instructions than comparing every lane with e and selecting.
+// lo/hi of lane e <- the wave-uniform 64-bit value v; other lanes keep theirs.  M0 holds
+// the lane (written by a scalar move, which v_writelane may use at once); the value
+// comes straight from the compare's scalar result, so no scalar instruction waits for a
+// vector one.
 __device__ __forceinline__ void stage_to_lane(uint32_t& lo, uint32_t& hi, uint64_t v, int e) {
-  uint64_t lane_mask, saved;
   asm volatile(
-      "s_lshl_b64 %[m], 1, %[e]\n\t"
-      "s_and_saveexec_b64 %[sv], %[m]\n\t"
-      "v_mov_b32 %[lo], %[vlo]\n\t"
-      "v_mov_b32 %[hi], %[vhi]\n\t"
-      "s_mov_b64 exec, %[sv]"
-      : [lo] "+v"(lo), [hi] "+v"(hi), [m] "=&s"(lane_mask), [sv] "=&s"(saved)
+      "s_mov_b32 m0, %[e]\n\t"
+      "v_writelane_b32 %[lo], %[vlo], m0\n\t"
+      "v_writelane_b32 %[hi], %[vhi], m0"
+      : [lo] "+v"(lo), [hi] "+v"(hi)
       : [e] "s"(e), [vlo] "s"((uint32_t)v), [vhi] "s"((uint32_t)(v >> 32))
-      : "scc");
+      : "m0");
 }
 
 // Where a wave's spikes go.
@@ -310,7 +308,7 @@ struct ConvSink {
 // global memory.  M32: candidate masks fit 32 bits (NC^2 <= 32).  NOTRUNC: no position
 // can hold max_queue_len events (max_queue_len >= the stream length), so every candidate
 // event is a real queue column.
-template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, int MODE, bool M32, bool NOTRUNC>
+template <int NIT, bool SAT, bool EXT, bool VTHN, int MODE, bool M32, bool NOTRUNC>
 __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
                                             const int (&vtc)[NIT], int n_ev, int base,
                                             const ConvSink& sk, int& vmin_l, int& vmax_l) {
@@ -320,7 +318,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   // stored once per chunk.
   uint32_t sg_lo[NIT], sg_hi[NIT];
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) { sg_lo[it] = 0; sg_hi[it] = 0; }
+  for (int it = 0; it < NIT; ++it) { sg_lo[it] = ~0u; sg_hi[it] = ~0u; }
   const int fa = qz.fa, rc = qz.rc;
   const uint32_t nt1 = (uint32_t)c.ntab + 1u;
   const int lane = threadIdx.x & (kWave - 1);
@@ -392,7 +390,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     uint64_t bal[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-      const int32_t d = decay_mul<F24>(o.v[it], o.A, fa, rc);
+      const int32_t d = decay_mul_wide(o.v[it], o.A, fa, rc);
       const int32_t u = (int32_t)((uint32_t)d + (uint32_t)o.qv[it]);  // codes hold q*2^f_V
       const int32_t f = fit_bits<SAT>(u, qz);
       const bool keep = f < o.vt[it];
@@ -403,8 +401,8 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
         lds_st<int32_t>(o.va + it * c.GiVSb + c.dmn, min(o.mnv[it], u));
         lds_st<int32_t>(o.va + it * c.GiVSb + c.dmx, max(o.mxv[it], u));
       }
-      // The spikes are the active lanes that did not keep their value: one compare.
-      bal[it] = __ballot(true) & ~__ballot(keep);
+      // Staged as the lanes that kept their value (the others spiked): one compare.
+      bal[it] = __ballot(keep);
     }
     asm volatile("" ::: "memory");  // the next event's reads come after these writes
     read_ops(o, rn, vcn, stn);
@@ -412,7 +410,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     for (int it = 0; it < NIT; ++it) {
       if (MODE == kStage) {
         stage_to_lane(sg_lo[it], sg_hi[it], bal[it], e);
-      } else if ((bal[it] >> lane) & 1) {
+      } else if (!((bal[it] >> lane) & 1)) {
         // Bit = candidate index in the event's NC x NC grid (compaction decodes it).
         const size_t w = ((size_t)sk.b * sk.L + r1.y) * (size_t)(sk.OC * sk.WPO) +
                          (size_t)(c.oc_lane + it * sk.Gi) * sk.WPO + (c.cand >> 5);
@@ -463,7 +461,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
 // at row stride Wp in LDS).  An empty position's catch-up has dt = 0; the identity
 // columns after it repeat V.  A full queue has no catch-up column.  Returns the largest
 // per-position event count.
-template <bool F24, bool EXT, bool TSPLIT>
+template <bool EXT, bool TSPLIT>
 __device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane& c, int lane,
                                            int T, int ocn, int PW, int W, int Wp, int VS,
                                            size_t v_base, int HW, int32_t* v_final,
@@ -485,7 +483,7 @@ __device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane& c, i
     int32_t mnn = EXT ? c.mn[vi] : 0, mxx = EXT ? c.mx[vi] : 0;
     if (st.y < c.mql) {
       const int dt = st.y > 0 ? T - st.x : 0;
-      vv = decay_mul<F24>(vv, c.ext[decay_slot(dt, c.ntab)], qz.fa, qz.rc);  // |D| <= |V|
+      vv = decay_mul_wide(vv, c.ext[decay_slot(dt, c.ntab)], qz.fa, qz.rc);  // |D| <= |V|
       vmin_l = min(vmin_l, vv);
       vmax_l = max(vmax_l, vv);
       mnn = min(mnn, vv);
@@ -501,7 +499,7 @@ __device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane& c, i
   return wave_max(maxcnt);
 }
 
-template <int NIT, bool F24, bool SAT, bool EXT, bool VTHN, bool M32, bool NOTRUNC>
+template <int NIT, bool SAT, bool EXT, bool VTHN, bool M32, bool NOTRUNC>
 __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(ConvArgs a) {
   extern __shared__ int32_t smem[];
   const ConvGeom& g = a.g;
@@ -643,11 +641,11 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
       if (lane == 0) red[dw * 4 + 3] = n_ev;
     }
     if (a.merge)
-      for (int i = lane; i < kWave * NIT; i += kWave) c.stg[i] = 0;
+      for (int i = lane; i < kWave * NIT; i += kWave) c.stg[i] = ~0ull;
     __syncthreads();
     if (!dec) n_ev = __builtin_amdgcn_readfirstlane(red[dw * 4 + 3]);
     if (a.merge) {
-      conv_events<NIT, F24, SAT, EXT, VTHN, kStage, M32, NOTRUNC>(qz, c, vtc, n_ev, base,
+      conv_events<NIT, SAT, EXT, VTHN, kStage, M32, NOTRUNC>(qz, c, vtc, n_ev, base,
                                                                    sk, vmin_l, vmax_l);
       __syncthreads();  // every wave's ballots of this chunk are staged
       if (wl == 0) {
@@ -660,7 +658,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
           for (int it = 0; it < NIT; ++it) {
             uint64_t bits = 0;
             for (int w = gi; w < nwps; w += a.ncg)
-              bits |= reinterpret_cast<const uint64_t*>(stg0 + w * lay.wave_words)[lane * NIT + it];
+              bits |= ~reinterpret_cast<const uint64_t*>(stg0 + w * lay.wave_words)[lane * NIT + it];
             cnt += __popcll(bits);
           }
         const int excl = wave_excl_scan(cnt, lane);
@@ -673,7 +671,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
             for (int it = 0; it < NIT; ++it) {
               uint64_t bits = 0;
               for (int w = gi; w < nwps; w += a.ncg)
-                bits |= reinterpret_cast<const uint64_t*>(stg0 + w * lay.wave_words)[lane * NIT + it];
+                bits |= ~reinterpret_cast<const uint64_t*>(stg0 + w * lay.wave_words)[lane * NIT + it];
               while (bits) {
                 const int k = __builtin_ctzll(bits);
                 bits &= bits - 1;
@@ -691,7 +689,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
       }
       __syncthreads();  // the staging and records are rewritten by the next chunk
     } else {
-      conv_events<NIT, F24, SAT, EXT, VTHN, kMask, M32, NOTRUNC>(qz, c, vtc, n_ev, base,
+      conv_events<NIT, SAT, EXT, VTHN, kMask, M32, NOTRUNC>(qz, c, vtc, n_ev, base,
                                                                   sk, vmin_l, vmax_l);
       __syncthreads();  // records are rewritten by the next chunk
     }
@@ -700,7 +698,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int T = n_eff > 0 ? time_ms(tb[n_eff - 1]) : 0;
   int maxcnt = 0;
   if (live)
-    maxcnt = conv_finish<F24, EXT, NOTRUNC>(qz, c, lane, T, ocn, PW, W, Wp, VS,
+    maxcnt = conv_finish<EXT, NOTRUNC>(qz, c, lane, T, ocn, PW, W, Wp, VS,
                                    (size_t)b * (g.OC * g.HW) + (size_t)oc0 * g.HW + r0 * W,
                                    g.HW, a.v_final, a.v_min, a.v_max, vmin_l, vmax_l);
   vmin_l = wave_min(vmin_l);

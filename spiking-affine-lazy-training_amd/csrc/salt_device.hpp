@@ -40,6 +40,15 @@ __device__ __forceinline__ int32_t decay_mul(int32_t v, int32_t a, int fa, int r
   return F24 ? __mul24(a, hi) + t2 : a * hi + t2;
 }
 
+// The same value as one 64-bit multiply-add: V*A = hi*A*2^f_a + lo*A, so
+// (V*A + c) >> f_a = hi*A + ((lo*A + c) >> f_a) exactly; |V| < 2^29 and A <= 2^f_a keep
+// the product in 64 bits and the result in 32.  Two instructions on gfx950
+// (v_mad_i64_i32, v_alignbit_b32) against six for the split form, which pays off in the
+// conv loop; the FC loop's chain is faster with the split form.
+__device__ __forceinline__ int32_t decay_mul_wide(int32_t v, int32_t a, int fa, int rc) {
+  return (int32_t)(((int64_t)v * a + rc) >> fa);
+}
+
 // Write-back into the (i_V + f_V)-bit register, salt_core/quant/fixed_point.py:68-90:
 // saturate clamps, wrap keeps the low wbits bits sign-extended.
 template <bool SAT>

@@ -580,7 +580,7 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
       if ((rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
       if ((rc = fill(reinterpret_cast<int32_t*>(a.masks), 0, need / 4, st))) return rc;
     }
-    const int flags = (f24 ? kConvF24 : 0) | (sat ? kConvSat : 0) | (ext ? kConvExt : 0) |
+    const int flags = (sat ? kConvSat : 0) | (ext ? kConvExt : 0) |
                       (prm->v_th_kind == SALT_VTH_PER_NEURON ? kConvVthN : 0) |
                       (pl.NC2 <= 32 ? kConvM32 : 0) |
                       (pl.tsplit ? kConvNoTrunc : 0);  // the layout follows this flag
