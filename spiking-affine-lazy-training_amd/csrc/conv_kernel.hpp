@@ -30,15 +30,16 @@
 // threshold.
 //
 // Output.  With the whole plane in the work-group, each wave stores the ballot of its
-// spikes per (chunk event, iteration) in LDS; after each 64-event chunk wave 0 ORs the
-// sub-bands' ballots (same lane mapping, disjoint candidate rows) and walks (event,
-// channel group, iteration, lane) = (event, ascending neuron id) -- the order of
-// salt_core/stream.py:24-46 -- appending to the stream.  With several work-groups per
-// stream (state above the LDS size) each wave sets per-event spike bits in global
-// memory instead, and a compaction kernel orders them.
+// spikes per (chunk event, iteration) and its spike count per chunk event in LDS; after
+// the chunk's barrier every wave places its own spikes in the stream's output, in the
+// order (event, channel group, iteration, lane) = (event, ascending neuron id) of
+// salt_core/stream.py:24-46, from a scan of all the stream's waves' counts.  With
+// several work-groups per stream (state above the LDS size) each wave sets per-event
+// spike bits in global memory instead, and a compaction kernel orders them.
 //
-// No barrier inside the event loop: a wave's LDS operations complete in program
-// order, so event e+1 reads what event e wrote.
+// One barrier per 64-event chunk, none inside the event loop: a wave's LDS operations
+// complete in program order, so event e+1 reads what event e wrote.  The decoding wave
+// decodes the next chunk while the others start this one (double-buffered records).
 #pragma once
 
 #include "salt_device.hpp"
@@ -90,14 +91,23 @@ struct ConvArgs {
 __host__ __device__ inline int conv_tcn(int PWs) { return PWs + kWave; }
 
 // LDS layout of a conv_layer_kernel work-group, in 4-byte words: a shared part (decay
-// table, ballot-bit map, reduction slots, int32 weight codes per channel group), then
+// table, ballot-bit map, reduction slots, int32 weight codes per channel group), one
+// region per (stream, sub-band) -- the decoded records and what the decode keeps -- then
 // one region per wave (spw streams x ncg x nsb waves).
 struct ConvLds {
-  int ext, lanemap, red, qs, shared_words;                        // shared
-  int rec, rec1, stg, tc, cnt, vthc, v, mn, mx, th, wave_words;   // per wave
+  int ext, lanemap, red, qs, shared_words;                      // shared
+  int rec, rec1, evt, nev, cnt, band_words;                     // per (stream, sub-band)
+  int stg, wcnt, tc, vthc, v, mn, mx, th, wave_words;           // per wave
+  int waves;  // word offset of the first wave region
   int vs, qst, tcn;
   int words;
 };
+
+// Record buffers (chunks in flight between the decode and the event loop) and event-info
+// buffers (chunks in flight between the decode and the output walk).
+constexpr int kConvRecBufs = 2;
+constexpr int kConvEvtBufs = 3;
+constexpr int kConvRecs = kWave + 2;  // a chunk's records and two that cover nothing
 
 // PWs: padded positions of a band (rows x Wp); vs >= PWs + NC2 and qs >= ICKK + 1: slot
 // strides (a slot's registers are followed by its NC2 spare words, its codes by a zero).
@@ -117,13 +127,20 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg
   l.qs = o;      o += ncg * Gp * l.qst;
   o = (o + 3) & ~3;
   l.shared_words = o;
-  int w = 0;
+  int bw = 0;
   // Two records more than a chunk's events: the loop reads two records ahead.
-  l.rec = w;  w += (kWave + 2) * 4;  // int4 {t, V base, weight base, candidate mask low}
-  l.rec1 = w; w += (kWave + 2) * 2;  // int2 {candidate mask high, event index}
-  l.stg = w;  w += kWave * nit * 2;  // uint64 spike ballot per (chunk event, iteration)
+  l.rec = bw;  bw += kConvRecBufs * kConvRecs * 4;  // int4 {t, V base, weight base, mask low}
+  l.rec1 = bw; bw += kConvRecBufs * kConvRecs * 2;  // int2 {mask high, event index}
+  l.evt = bw;  bw += kConvEvtBufs * kWave * 2;      // int2 {t, plane position} per chunk event
+  l.nev = bw;  bw += 4;                             // events with a candidate, per record buffer
+  l.cnt = bw;  bw += tsplit ? PWs : 0;              // queue counts (tsplit)
+  bw = (bw + 3) & ~3;
+  l.band_words = bw;
+  l.waves = l.shared_words + spw * nsb * bw;
+  int w = 0;
+  l.stg = w;  w += 2 * kWave * nit * 2;  // uint64 spike ballot per (chunk event, iteration), x2
+  l.wcnt = w; w += 2 * kWave;            // spikes per chunk event, x2
   l.tc = w;   w += (tsplit ? 1 : 2) * l.tcn;  // {last-update time, queue count} or time
-  l.cnt = w;  w += tsplit ? PWs : 0;          // queue counts (tsplit)
   l.vthc = w; w += Gp;
   l.v = w;    w += Gp * l.vs;
   l.mn = w;   w += ext ? Gp * l.vs : 0;
@@ -131,7 +148,7 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg
   l.th = w;   w += vthn ? Gp * l.vs : 0;
   w = (w + 3) & ~3;
   l.wave_words = w;
-  l.words = l.shared_words + spw * ncg * nsb * w;
+  l.words = l.waves + spw * ncg * nsb * w;
   return l;
 }
 
@@ -143,7 +160,8 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg
 struct ConvLane {
   int4* rec;
   int2* rec1;
-  uint64_t* stg;
+  uint64_t* stg;         // this chunk's spike ballots (kStage)
+  int32_t* wcnt;         // this chunk's spikes per event (kStage)
   int2* tc;
   const int32_t* ext;
   const int32_t* qs;     // weight codes q*2^f_V
@@ -312,6 +330,15 @@ template <int NIT, bool SAT, bool EXT, bool VTHN, int MODE, bool M32, bool NOTRU
 __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
                                             const int (&vtc)[NIT], int n_ev, int base,
                                             const ConvSink& sk, int& vmin_l, int& vmax_l) {
+  const int lane = threadIdx.x & (kWave - 1);
+  // kStage: the chunk's ballots and spike counts, indexed by the event's place in the
+  // chunk: events without a candidate in this sub-band keep "no spike".  These clears
+  // precede the events' entries (a wave's LDS writes complete in order).
+  if (MODE == kStage) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) c.stg[lane * NIT + it] = ~0ull;
+    c.wcnt[lane] = 0;
+  }
   if (n_ev == 0) return;
   constexpr bool kRec1 = !M32 || MODE == kMask;  // the loop needs the second record word
   // kStage: lane e of sg_lo/sg_hi[it] collects event e's spike ballot; they are
@@ -321,7 +348,6 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   for (int it = 0; it < NIT; ++it) { sg_lo[it] = ~0u; sg_hi[it] = ~0u; }
   const int fa = qz.fa, rc = qz.rc;
   const uint32_t nt1 = (uint32_t)c.ntab + 1u;
-  const int lane = threadIdx.x & (kWave - 1);
   const uint32_t lm32 = (uint32_t)c.lm;
   auto covers = [&](const int4& r, const int2& r1) -> bool {
     if (M32) return ((uint32_t)r.w & lm32) != 0u;
@@ -450,9 +476,14 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   __builtin_amdgcn_s_setprio(3);
   if (MODE == kStage && lane < n_ev) {
     const int jc = c.rec1[lane].y - base;  // the event's index within the chunk
+    int nsp = 0;
 #pragma unroll
-    for (int it = 0; it < NIT; ++it)
-      c.stg[jc * NIT + it] = ((uint64_t)sg_hi[it] << 32) | sg_lo[it];
+    for (int it = 0; it < NIT; ++it) {
+      const uint64_t kept = ((uint64_t)sg_hi[it] << 32) | sg_lo[it];
+      c.stg[jc * NIT + it] = kept;
+      nsp += __popcll(~kept);
+    }
+    c.wcnt[jc] = nsp;
   }
 }
 
@@ -525,10 +556,20 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const ConvLds lay = conv_lds_layout(qz.n_table, a.spw, a.ncg, a.nsb, Gp, NIT, a.VS, a.QS,
                                       PWs, EXT, VTHN, NOTRUNC);
   const int VS = lay.vs, QS = lay.qst;
-  int32_t* wbase = smem + lay.shared_words + wv * lay.wave_words;
+  // regions: this (stream, sub-band)'s, the stream's sub-band 0's, this wave's, and the
+  // stream's first wave's
+  int32_t* const band = smem + lay.shared_words + (ks * a.nsb + sb) * lay.band_words;
+  int32_t* const band0 = smem + lay.shared_words + ks * a.nsb * lay.band_words;
+  int32_t* const wbase = smem + lay.waves + wv * lay.wave_words;
+  const int32_t* const swave0 = smem + lay.waves + ks * nwps * lay.wave_words;
   int2* lanemap = reinterpret_cast<int2*>(smem + lay.lanemap);
   int32_t* red = smem + lay.red;
   int32_t* ext = smem + lay.ext;
+  int4* const recs = reinterpret_cast<int4*>(band + lay.rec);
+  int2* const recs1 = reinterpret_cast<int2*>(band + lay.rec1);
+  int32_t* const nev = band + lay.nev;
+  int2* const evt0 = reinterpret_cast<int2*>(band0 + lay.evt);
+  uint64_t* const stgs = reinterpret_cast<uint64_t*>(wbase + lay.stg);
   ConvLane c;
   c.ext = ext;
   c.qs = smem + lay.qs + cg * Gp * QS;
@@ -536,13 +577,8 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   // keeps the queue counts); the other channel groups see the same events and read its
   // records.
   const bool dec = cg == 0;
-  const int dw = ks * nwps + sb * a.ncg;  // the decoding wave
-  int32_t* const dbase = smem + lay.shared_words + dw * lay.wave_words;
-  c.rec = reinterpret_cast<int4*>(dbase + lay.rec);
-  c.rec1 = reinterpret_cast<int2*>(dbase + lay.rec1);
-  c.stg = reinterpret_cast<uint64_t*>(wbase + lay.stg);
   c.tc = reinterpret_cast<int2*>(wbase + lay.tc);
-  c.cnt = dbase + lay.cnt;
+  c.cnt = band + lay.cnt;
   int32_t* const cnt_kept = (NOTRUNC && dec) ? c.cnt : nullptr;
   int32_t* vthc = wbase + lay.vthc;
   c.Vs = wbase + lay.v;
@@ -586,18 +622,18 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     }
   }
   for (int i = lane; i < (NOTRUNC ? 1 : 2) * lay.tcn; i += kWave) wbase[lay.tc + i] = 0;
-  if (NOTRUNC)
-    for (int i = lane; i < PWs; i += kWave) wbase[lay.cnt + i] = 0;
-  if (dec && lane < 2) {  // the records after a full chunk: no candidate
-    c.rec[kWave + lane] = make_int4(0, 0, 0, 0);
-    c.rec1[kWave + lane] = make_int2(0, 0);
+  if (dec) {
+    if (NOTRUNC)
+      for (int i = lane; i < PWs; i += kWave) c.cnt[i] = 0;
+    if (lane < 2)  // the records after a full chunk: no candidate
+      for (int bf = 0; bf < kConvRecBufs; ++bf) {
+        recs[bf * kConvRecs + kWave + lane] = make_int4(0, 0, 0, 0);
+        recs1[bf * kConvRecs + kWave + lane] = make_int2(0, 0);
+      }
   }
-  __syncthreads();
 
   conv_lane_setup(c, g, lane, Gi, VS, QS, PWs, oc0, qz.n_table, NOTRUNC ? 4 : 8, smem);
   int vtc[NIT];
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) vtc[it] = vthc[min(it * Gi + c.oc_lane - oc0, Gp - 1)];
   ConvSink sk;
   sk.b = b; sk.masks = a.masks; sk.L = a.L; sk.OC = g.OC; sk.WPO = a.WPO; sk.Gi = Gi;
 
@@ -612,88 +648,119 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   int n_grp = 0;
   for (int i = lane; i < a.spw; i += kWave) n_grp = max(n_grp, real_count(blockIdx.y * a.spw + i));
   n_grp = __builtin_amdgcn_readfirstlane(wave_max(n_grp));
+  const int nchunks = (n_grp + kWave - 1) / kWave;
   const float* tb = a.times + (size_t)(live ? b : 0) * L;
   const int32_t* sb_src = a.src + (size_t)(live ? b : 0) * L;
 
   int vmin_l = 0, vmax_l = 0;
-  int out_base = 0;  // spikes emitted so far (the stream's first wave, merge mode)
+  int out_base = 0;  // spikes of the stream emitted so far (merge mode)
 
-  // Next chunk of events, loaded one chunk ahead and converted only when its chunk
-  // starts, so the loads' latency is covered by a chunk of work.  The index is clamped
+  // Next chunk of events, loaded one chunk ahead and converted only when its chunk is
+  // decoded, so the loads' latency is covered by a chunk of work.  The index is clamped
   // into the stream (entries past n_eff are not real: conv_decode checks j < n_eff);
   // a stream without events loads nothing.
   const int jl = n_eff - 1;
   float t_n = 0.0f;
   int s_n = -1;
   if (dec && jl >= 0) { t_n = tb[min(lane, jl)]; s_n = sb_src[min(lane, jl)]; }
-
-  for (int base = 0; base < n_grp; base += kWave) {
-    const int j = base + lane;
+  // Decoding wave: chunk k into record buffer k % 2 (and, merge mode, sub-band 0: the
+  // chunk's event times and plane positions into event buffer k % 3).
+  auto decode = [&](int k) {
+    const int bf = k & 1;
+    const int j = k * kWave + lane;
     const int tv = time_ms(t_n), sv = s_n;
-    int oy0 = 0, ox0 = 0, n_ev = 0;
-    if (dec) {
-      if (jl >= 0) {
-        const int j2 = min(j + kWave, jl);
-        t_n = tb[j2];
-        s_n = sb_src[j2];
-      }
-      n_ev = conv_decode(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0, cnt_kept);
-      if (lane == 0) red[dw * 4 + 3] = n_ev;
+    if (jl >= 0) {
+      const int j2 = min(j + kWave, jl);
+      t_n = tb[j2];
+      s_n = sb_src[j2];
     }
-    if (a.merge)
-      for (int i = lane; i < kWave * NIT; i += kWave) c.stg[i] = ~0ull;
-    __syncthreads();
-    if (!dec) n_ev = __builtin_amdgcn_readfirstlane(red[dw * 4 + 3]);
-    if (a.merge) {
-      conv_events<NIT, SAT, EXT, VTHN, kStage, M32, NOTRUNC>(qz, c, vtc, n_ev, base,
-                                                                   sk, vmin_l, vmax_l);
-      __syncthreads();  // every wave's ballots of this chunk are staged
-      if (wl == 0) {
-        // The stream's first wave walks (event, channel group, iteration, bit) = (event,
-        // ascending neuron id); the sub-bands' ballots of one event are disjoint and
-        // share the lane mapping.
-        const int32_t* stg0 = smem + lay.shared_words + ks * nwps * lay.wave_words + lay.stg;
-        int cnt = 0;
-        for (int gi = 0; gi < a.ncg; ++gi)
-          for (int it = 0; it < NIT; ++it) {
-            uint64_t bits = 0;
-            for (int w = gi; w < nwps; w += a.ncg)
-              bits |= ~reinterpret_cast<const uint64_t*>(stg0 + w * lay.wave_words)[lane * NIT + it];
-            cnt += __popcll(bits);
-          }
-        const int excl = wave_excl_scan(cnt, lane);
-        const int total = wave_sum(cnt);
-        if (cnt > 0) {
-          const float te = (float)tv;
-          const int pg = oy0 * W + ox0;  // plane position of the event's first candidate
-          int pos = out_base + excl;
-          for (int gi = 0; gi < a.ncg; ++gi)
-            for (int it = 0; it < NIT; ++it) {
-              uint64_t bits = 0;
-              for (int w = gi; w < nwps; w += a.ncg)
-                bits |= ~reinterpret_cast<const uint64_t*>(stg0 + w * lay.wave_words)[lane * NIT + it];
-              while (bits) {
-                const int k = __builtin_ctzll(bits);
-                bits &= bits - 1;
-                const int2 lmk = lanemap[k];
-                const int oc = gi * a.G + it * Gi + lmk.x;
-                if (pos < a.cap) {
-                  a.out_t[(size_t)b * a.cap + pos] = te;
-                  a.out_s[(size_t)b * a.cap + pos] = oc * g.HW + pg + lmk.y;
-                }
-                ++pos;
-              }
-            }
+    c.rec = recs + bf * kConvRecs;
+    c.rec1 = recs1 + bf * kConvRecs;
+    int oy0 = 0, ox0 = 0;
+    const int n = conv_decode(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0, cnt_kept);
+    if (lane == 0) nev[bf] = n;
+    if (a.merge && sb == 0) evt0[(k % kConvEvtBufs) * kWave + lane] = make_int2(tv, oy0 * W + ox0);
+  };
+  // Merge mode, every wave: its own spikes of chunk k, at their places in the stream's
+  // output, ordered (event, channel group, iteration, bit) = (event, ascending neuron id)
+  // -- the order of salt_core/stream.py:24-46.  Lane = the event's index in the chunk.
+  // An event's spikes start after those of the chunk's earlier events (a scan of the
+  // stream's waves' counts) and, within it, after the lower channel groups' spikes and
+  // this group's lower iterations and bits; the sub-bands' ballots of one channel group
+  // are disjoint and share the lane mapping, so the bits below a spike are counted in
+  // their union.
+  auto walk = [&](int k) {
+    const int bf = k & 1;
+    int tot = 0, before = 0;
+    for (int w = 0; w < nwps; ++w) {
+      const int cw = swave0[w * lay.wave_words + lay.wcnt + bf * kWave + lane];
+      tot += cw;
+      before += (w % a.ncg < cg) ? cw : 0;
+    }
+    if (__ballot(tot != 0) == 0) return;  // no spike in the chunk
+    int incl = tot;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int t = __shfl_up(incl, o);
+      incl += lane >= o ? t : 0;
+    }
+    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+    const int2 ev = evt0[(k % kConvEvtBufs) * kWave + lane];  // read with every lane active
+    const float te = (float)ev.x;
+    int pos = out_base + (incl - tot) + before;
+    const uint64_t* const stg_cg = reinterpret_cast<const uint64_t*>(
+        swave0 + cg * lay.wave_words + lay.stg) + bf * kWave * NIT + lane * NIT;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      uint64_t all = 0, mine = 0;
+      for (int s2 = 0; s2 < a.nsb; ++s2) {
+        const uint64_t v = ~stg_cg[s2 * a.ncg * (lay.wave_words / 2) + it];
+        all |= v;
+        mine = s2 == sb ? v : mine;
+      }
+      while (mine) {
+        const int kb = __builtin_ctzll(mine);
+        mine &= mine - 1;
+        const int p = pos + __popcll(all & ((1ull << kb) - 1));
+        const int2 lmk = lanemap[kb];
+        const int oc = oc0 + it * Gi + lmk.x;
+        if (p < a.cap) {
+          a.out_t[(size_t)b * a.cap + p] = te;
+          a.out_s[(size_t)b * a.cap + p] = oc * g.HW + ev.y + lmk.y;
         }
-        out_base += total;
       }
-      __syncthreads();  // the staging and records are rewritten by the next chunk
-    } else {
-      conv_events<NIT, SAT, EXT, VTHN, kMask, M32, NOTRUNC>(qz, c, vtc, n_ev, base,
-                                                                  sk, vmin_l, vmax_l);
-      __syncthreads();  // records are rewritten by the next chunk
+      pos += __popcll(all);
     }
+    out_base += total;
+  };
+
+  if (dec && nchunks > 0) decode(0);
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) vtc[it] = vthc[min(it * Gi + c.oc_lane - oc0, Gp - 1)];
+  // One barrier per chunk: chunk k's records and counts were written before the last
+  // barrier; the next chunk's decode writes the other record buffer, whose readers
+  // finished before it; the walk of chunk k-1 reads the ballots and counts written
+  // before it, and event info decoded two chunks before the next decode's.
+  for (int k = 0; k < nchunks; ++k) {
+    const int bf = k & 1;
+    if (dec && k + 1 < nchunks) decode(k + 1);
+    if (a.merge && k > 0) walk(k - 1);
+    c.rec = recs + bf * kConvRecs;
+    c.rec1 = recs1 + bf * kConvRecs;
+    const int n_ev = __builtin_amdgcn_readfirstlane(nev[bf]);
+    if (a.merge) {
+      c.stg = stgs + bf * kWave * NIT;
+      c.wcnt = wbase + lay.wcnt + bf * kWave;
+      conv_events<NIT, SAT, EXT, VTHN, kStage, M32, NOTRUNC>(qz, c, vtc, n_ev, k * kWave,
+                                                                   sk, vmin_l, vmax_l);
+    } else {
+      conv_events<NIT, SAT, EXT, VTHN, kMask, M32, NOTRUNC>(qz, c, vtc, n_ev, k * kWave,
+                                                                  sk, vmin_l, vmax_l);
+    }
+    __syncthreads();
   }
+  if (a.merge && nchunks > 0) walk(nchunks - 1);
 
   const int T = n_eff > 0 ? time_ms(tb[n_eff - 1]) : 0;
   int maxcnt = 0;
