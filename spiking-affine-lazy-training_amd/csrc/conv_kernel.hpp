@@ -698,12 +698,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
       before += (w % a.ncg < cg) ? cw : 0;
     }
     if (__ballot(tot != 0) == 0) return;  // no spike in the chunk
-    int incl = tot;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const int t = __shfl_up(incl, o);
-      incl += lane >= o ? t : 0;
-    }
+    const int incl = wave_incl_scan(tot);
     const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
     const int2 ev = evt0[(k % kConvEvtBufs) * kWave + lane];  // read with every lane active
     const float te = (float)ev.x;

@@ -94,8 +94,9 @@ __global__ void __launch_bounds__(64) compact_kernel(CompactArgs a) {
     int count = 0;
     if (ok)
       for (int w = 0; w < a.words; ++w) count += __popc(m[w]);
-    const int excl = wave_excl_scan(count, lane);
-    const int total = wave_sum(count);
+    const int incl = wave_incl_scan(count);
+    const int excl = incl - count;
+    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
     if (ok && count > 0) {
       int pos = out_base + excl;
       const float te = a.times[(size_t)b * L + j];
