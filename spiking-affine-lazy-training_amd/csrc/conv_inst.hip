@@ -15,11 +15,16 @@ template <int NIT, int F>
 hipError_t conv_entry(const ConvArgs& a, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
   constexpr bool kSat = (F & kConvSat) != 0,
                  kExt = (F & kConvExt) != 0, kVthN = (F & kConvVthN) != 0,
-                 kM32 = (F & kConvM32) != 0, kNoTrunc = (F & kConvNoTrunc) != 0;
-  static bool attr_set = false;
-  auto fn = conv_layer_kernel<NIT, kSat, kExt, kVthN, kM32, kNoTrunc>;
-  return launch_with_lds(reinterpret_cast<const void*>(fn), fn, &attr_set, grid, block, lds, st,
-                         a);
+                 kM32 = (F & kConvM32) != 0, kNoTrunc = (F & kConvNoTrunc) != 0,
+                 kPair = (F & kConvPair) != 0;
+  if constexpr (kPair && !kM32) {
+    return hipErrorInvalidValue;  // pairs need candidate masks of 32 bits or less
+  } else {
+    static bool attr_set = false;
+    auto fn = conv_layer_kernel<NIT, kSat, kExt, kVthN, kM32, kNoTrunc, kPair>;
+    return launch_with_lds(reinterpret_cast<const void*>(fn), fn, &attr_set, grid, block, lds,
+                           st, a);
+  }
 }
 
 using ConvFn = hipError_t (*)(const ConvArgs&, dim3, dim3, size_t, hipStream_t);

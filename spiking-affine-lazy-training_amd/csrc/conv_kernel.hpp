@@ -107,15 +107,19 @@ struct ConvLds {
 // buffers (chunks in flight between the decode and the output walk).
 constexpr int kConvRecBufs = 2;
 constexpr int kConvEvtBufs = 3;
-constexpr int kConvRecs = kWave + 2;  // a chunk's records and two that cover nothing
+// Records per buffer: a chunk's steps and two steps that cover nothing, one record per
+// step, or two (pair: the events of the step's two half-waves).
+__host__ __device__ inline int conv_recs(bool pair) { return (pair ? 2 : 1) * (kWave + 2); }
 
 // PWs: padded positions of a band (rows x Wp); vs >= PWs + NC2 and qs >= ICKK + 1: slot
 // strides (a slot's registers are followed by its NC2 spare words, its codes by a zero).
 // tsplit (no queue truncation possible): the per-position entries are last-update times
 // alone, and the queue counts a separate array (kept by the decode, read at the end).
+// pair: two events per step (one per half-wave).
 __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg, int nsb,
                                                    int Gp, int nit, int vs, int qs, int PWs,
-                                                   bool ext, bool vthn, bool tsplit) {
+                                                   bool ext, bool vthn, bool tsplit,
+                                                   bool pair) {
   ConvLds l;
   l.vs = vs;
   l.qst = qs;
@@ -128,11 +132,12 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg
   o = (o + 3) & ~3;
   l.shared_words = o;
   int bw = 0;
-  // Two records more than a chunk's events: the loop reads two records ahead.
-  l.rec = bw;  bw += kConvRecBufs * kConvRecs * 4;  // int4 {t, V base, weight base, mask low}
-  l.rec1 = bw; bw += kConvRecBufs * kConvRecs * 2;  // int2 {mask high, event index}
+  // Two steps more than a chunk's events: the loop reads two steps ahead.
+  const int nrec = kConvRecBufs * conv_recs(pair);
+  l.rec = bw;  bw += nrec * 4;                      // int4 {t, V base, weight base, mask low}
+  l.rec1 = bw; bw += nrec * 2;                      // int2 {mask high, event index}
   l.evt = bw;  bw += kConvEvtBufs * kWave * 2;      // int2 {t, plane position} per chunk event
-  l.nev = bw;  bw += 4;                             // events with a candidate, per record buffer
+  l.nev = bw;  bw += 4;                             // steps of the chunk, per record buffer
   l.cnt = bw;  bw += tsplit ? PWs : 0;              // queue counts (tsplit)
   bw = (bw + 3) & ~3;
   l.band_words = bw;
@@ -171,6 +176,7 @@ struct ConvLane {
   int32_t* th;
   int32_t* cnt;         // tsplit: queue counts of the band's positions
   uint64_t lm;          // this lane's candidate bit (0 for lanes without a slot)
+  int rh;               // pair: the lane's record of a step (its half-wave), else 0
   int lp, lv, lq;       // position / register / code offsets relative to an event's bases
   int v_spare, q_zero, tc_spare;  // this lane's spare register word, zero code, spare entry
   int GiVS, GiQS;
@@ -190,12 +196,16 @@ __device__ __forceinline__ uint32_t lds_addr(const int32_t* p) {
 
 // Lane constants for a wave of Gi slots per iteration over a band of PWs positions
 // (slot strides VS / QS), whose first channel is oc0; tcb: bytes per (time, count)
-// entry (8, or 4 for times alone).  base: the work-group's LDS.
+// entry (8, or 4 for times alone).  base: the work-group's LDS.  pair: each half-wave
+// holds the same Gi slots for its own event.
 __device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, int lane,
                                                 int Gi, int VS, int QS, int PWs, int oc0,
-                                                int ntab, int tcb, const int32_t* base) {
-  const int slot0 = lane / g.NC2;
-  c.cand = lane - slot0 * g.NC2;
+                                                int ntab, int tcb, const int32_t* base,
+                                                bool pair) {
+  const int ll = pair ? (lane & 31) : lane;  // the lane among its event's lanes
+  const int slot0 = ll / g.NC2;
+  c.cand = ll - slot0 * g.NC2;
+  c.rh = pair ? lane >> 5 : 0;
   const int dy = c.cand / g.NC, dx = c.cand - (c.cand / g.NC) * g.NC;
   const bool lane_on = slot0 < Gi;
   const int slot_t = lane_on ? slot0 : 0;
@@ -260,6 +270,9 @@ __device__ __forceinline__ void lds_st_tc(int addr, int t, int cnt) {
 // candidate; oy0/ox0 = the event's first candidate row and column.
 // cnt (queue counts of a wave that keeps them, else null): each event adds one to the
 // count of every candidate position it has.
+// PAIR: the records go to steps of two events instead, and the number of steps is
+// returned (see below).
+template <bool PAIR>
 __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c, int tv,
                                            int sv, int j, int n_eff, int r0, int rn, int& oy0,
                                            int& ox0, int32_t* cnt) {
@@ -292,9 +305,48 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
   const uint64_t relm = __ballot(rel);
   const int n = __popcll(relm);
   const int slot = rel ? lanes_below(relm) : n + lanes_below(~relm);
-  c.rec[slot] = make_int4(tv, p0 * 4, q0 * 4, (int)(uint32_t)m);
-  c.rec1[slot] = make_int2((int)(uint32_t)(m >> 32), j);
-  return n;
+  if (!PAIR) {
+    c.rec[slot] = make_int4(tv, p0 * 4, q0 * 4, (int)(uint32_t)m);
+    c.rec1[slot] = make_int2((int)(uint32_t)(m >> 32), j);
+    return n;
+  }
+  // Pairs (candidate masks of 32 bits or less).  Two events whose candidate blocks are
+  // NC or more rows or columns apart touch disjoint positions, so they can be updated
+  // at once, one per half-wave, with the results of updating them in order.  The
+  // relevant events are taken in order, greedily: event i shares a step with event i+1
+  // when the two are disjoint and i does not already share one with i-1.  Bit i of D:
+  // relevant events i and i+1 are disjoint; within each run of set bits the pairs start
+  // at the run's first bit and every second bit after it, i.e. at the bits with the
+  // parity of the run's start.
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint64_t above = relm & ~((2ull << lane) - 1ull);  // relevant events after this one
+  const int nxt = above ? __builtin_ctzll(above) : lane;
+  const int oyn = __shfl(oy0, nxt), oxn = __shfl(ox0, nxt);
+  const bool dis = rel && above != 0 && (abs(oyn - oy0) >= g.NC || abs(oxn - ox0) >= g.NC);
+  // to lane = index among the relevant events (slot is a permutation of the lanes)
+  const int dis_i = __builtin_amdgcn_ds_permute(slot << 2, dis ? 1 : 0);
+  const uint64_t D = __ballot(dis_i != 0);
+  constexpr uint64_t kEven = 0x5555555555555555ull;
+  const uint64_t starts = D & ~(D << 1);
+  // adding a run's start bit clears the run (the carry stops at the 0 after it)
+  const uint64_t even_runs = D & ~(D + (starts & kEven));
+  const uint64_t firsts = (even_runs & kEven) | (D & ~even_runs & ~kEven);
+  const uint64_t seconds = firsts << 1;
+  // relevant event i -> record 2 * step + half, step = i - (second events up to i)
+  const int sec = (int)((seconds >> lane) & 1ull);
+  const int place = 2 * (lane - lanes_below(seconds) - sec) + sec;
+  const int rp = __shfl(place, slot);
+  // every record of the chunk's steps covers nothing, then the events' (a wave's LDS
+  // writes complete in order)
+  c.rec[2 * lane] = make_int4(0, 0, 0, 0);
+  c.rec[2 * lane + 1] = make_int4(0, 0, 0, 0);
+  c.rec1[2 * lane] = make_int2(0, -1);
+  c.rec1[2 * lane + 1] = make_int2(0, -1);
+  if (rel) {
+    c.rec[rp] = make_int4(tv, p0 * 4, q0 * 4, (int)(uint32_t)m);
+    c.rec1[rp] = make_int2(0, j);
+  }
+  return n - __popcll(seconds);
 }
 
 // lo/hi of lane e <- the wave-uniform 64-bit value v; other lanes keep theirs.  M0 holds
@@ -325,8 +377,9 @@ struct ConvSink {
 // kStage: stage the spike ballots for the work-group's merge; kMask: set spike bits in
 // global memory.  M32: candidate masks fit 32 bits (NC^2 <= 32).  NOTRUNC: no position
 // can hold max_queue_len events (max_queue_len >= the stream length), so every candidate
-// event is a real queue column.
-template <int NIT, bool SAT, bool EXT, bool VTHN, int MODE, bool M32, bool NOTRUNC>
+// event is a real queue column.  PAIR: n_ev steps of two events, one per half-wave (a
+// step's second record covers nothing when it has one event).
+template <int NIT, bool SAT, bool EXT, bool VTHN, int MODE, bool M32, bool NOTRUNC, bool PAIR>
 __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
                                             const int (&vtc)[NIT], int n_ev, int base,
                                             const ConvSink& sk, int& vmin_l, int& vmax_l) {
@@ -389,13 +442,16 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
       }
     }
   };
-  int4 r = c.rec[0];
-  int2 r1 = kRec1 ? c.rec1[0] : make_int2(0, 0);
+  // this lane's record of step e: rec[RS * e + rh]
+  constexpr int RS = PAIR ? 2 : 1;
+  const int rh = PAIR ? c.rh : 0;
+  int4 r = c.rec[rh];
+  int2 r1 = kRec1 ? c.rec1[rh] : make_int2(0, 0);
   bool vc = covers(r, r1);
   int pab = (r.y << kTcShift) + c.ltb;  // this lane's (time, count) entry for the event
   int2 st = tc_load(vc ? pab : c.tc_common_b);
-  int4 rn = c.rec[1];  // records past the last event cover nothing
-  int2 rn1 = kRec1 ? c.rec1[1] : make_int2(0, 0);
+  int4 rn = c.rec[RS + rh];  // records past the last step cover nothing
+  int2 rn1 = kRec1 ? c.rec1[RS + rh] : make_int2(0, 0);
   Ops o;
   read_ops(o, r, vc, st);
   // One event; everything carried becomes the next event's.
@@ -410,8 +466,8 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     const bool vcn = covers(rn, rn1);
     const int pabn = (rn.y << kTcShift) + c.ltb;
     const int2 stn = tc_load(vcn ? pabn : c.tc_common_b);
-    const int4 rn2 = c.rec[e + 2];
-    const int2 rn12 = kRec1 ? c.rec1[e + 2] : make_int2(0, 0);
+    const int4 rn2 = c.rec[RS * (e + 2) + rh];
+    const int2 rn12 = kRec1 ? c.rec1[RS * (e + 2) + rh] : make_int2(0, 0);
     asm volatile("" ::: "memory");  // the reads above go out before this event's update
     uint64_t bal[NIT];
 #pragma unroll
@@ -474,7 +530,23 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     if (e < end) event(e++);
   }
   __builtin_amdgcn_s_setprio(3);
-  if (MODE == kStage && lane < n_ev) {
+  if (PAIR && MODE == kStage && lane < n_ev) {
+    // step lane: half-wave h's ballot bits belong to the event of record 2 * lane + h
+    const int j0 = c.rec1[2 * lane].y - base, j1 = c.rec1[2 * lane + 1].y;
+    int n0 = 0, n1 = 0;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const uint64_t k0 = 0xffffffff00000000ull | sg_lo[it];
+      const uint64_t k1 = 0xffffffff00000000ull | sg_hi[it];
+      c.stg[j0 * NIT + it] = k0;
+      n0 += __popcll(~k0);
+      if (j1 >= 0) c.stg[(j1 - base) * NIT + it] = k1;
+      n1 += __popcll(~k1);
+    }
+    c.wcnt[j0] = n0;
+    if (j1 >= 0) c.wcnt[j1 - base] = n1;
+  }
+  if (!PAIR && MODE == kStage && lane < n_ev) {
     const int jc = c.rec1[lane].y - base;  // the event's index within the chunk
     int nsp = 0;
 #pragma unroll
@@ -530,7 +602,7 @@ __device__ __forceinline__ int conv_finish(const Quant& qz, const ConvLane& c, i
   return wave_max(maxcnt);
 }
 
-template <int NIT, bool SAT, bool EXT, bool VTHN, bool M32, bool NOTRUNC>
+template <int NIT, bool SAT, bool EXT, bool VTHN, bool M32, bool NOTRUNC, bool PAIR>
 __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(ConvArgs a) {
   extern __shared__ int32_t smem[];
   const ConvGeom& g = a.g;
@@ -554,8 +626,9 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int ICKK = g.IC * g.K * g.K;
   const Quant& qz = a.qz;
   const ConvLds lay = conv_lds_layout(qz.n_table, a.spw, a.ncg, a.nsb, Gp, NIT, a.VS, a.QS,
-                                      PWs, EXT, VTHN, NOTRUNC);
+                                      PWs, EXT, VTHN, NOTRUNC, PAIR);
   const int VS = lay.vs, QS = lay.qst;
+  constexpr int RS = PAIR ? 2 : 1;  // records per step
   // regions: this (stream, sub-band)'s, the stream's sub-band 0's, this wave's, and the
   // stream's first wave's
   int32_t* const band = smem + lay.shared_words + (ks * a.nsb + sb) * lay.band_words;
@@ -625,14 +698,14 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   if (dec) {
     if (NOTRUNC)
       for (int i = lane; i < PWs; i += kWave) c.cnt[i] = 0;
-    if (lane < 2)  // the records after a full chunk: no candidate
+    if (lane < 2 * RS)  // the records after a full chunk: no candidate
       for (int bf = 0; bf < kConvRecBufs; ++bf) {
-        recs[bf * kConvRecs + kWave + lane] = make_int4(0, 0, 0, 0);
-        recs1[bf * kConvRecs + kWave + lane] = make_int2(0, 0);
+        recs[bf * conv_recs(PAIR) + RS * kWave + lane] = make_int4(0, 0, 0, 0);
+        recs1[bf * conv_recs(PAIR) + RS * kWave + lane] = make_int2(0, -1);
       }
   }
 
-  conv_lane_setup(c, g, lane, Gi, VS, QS, PWs, oc0, qz.n_table, NOTRUNC ? 4 : 8, smem);
+  conv_lane_setup(c, g, lane, Gi, VS, QS, PWs, oc0, qz.n_table, NOTRUNC ? 4 : 8, smem, PAIR);
   int vtc[NIT];
   ConvSink sk;
   sk.b = b; sk.masks = a.masks; sk.L = a.L; sk.OC = g.OC; sk.WPO = a.WPO; sk.Gi = Gi;
@@ -674,10 +747,10 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
       t_n = tb[j2];
       s_n = sb_src[j2];
     }
-    c.rec = recs + bf * kConvRecs;
-    c.rec1 = recs1 + bf * kConvRecs;
+    c.rec = recs + bf * conv_recs(PAIR);
+    c.rec1 = recs1 + bf * conv_recs(PAIR);
     int oy0 = 0, ox0 = 0;
-    const int n = conv_decode(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0, cnt_kept);
+    const int n = conv_decode<PAIR>(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0, cnt_kept);
     if (lane == 0) nev[bf] = n;
     if (a.merge && sb == 0) evt0[(k % kConvEvtBufs) * kWave + lane] = make_int2(tv, oy0 * W + ox0);
   };
@@ -741,17 +814,17 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     const int bf = k & 1;
     if (dec && k + 1 < nchunks) decode(k + 1);
     if (a.merge && k > 0) walk(k - 1);
-    c.rec = recs + bf * kConvRecs;
-    c.rec1 = recs1 + bf * kConvRecs;
+    c.rec = recs + bf * conv_recs(PAIR);
+    c.rec1 = recs1 + bf * conv_recs(PAIR);
     const int n_ev = __builtin_amdgcn_readfirstlane(nev[bf]);
     if (a.merge) {
       c.stg = stgs + bf * kWave * NIT;
       c.wcnt = wbase + lay.wcnt + bf * kWave;
-      conv_events<NIT, SAT, EXT, VTHN, kStage, M32, NOTRUNC>(qz, c, vtc, n_ev, k * kWave,
-                                                                   sk, vmin_l, vmax_l);
+      conv_events<NIT, SAT, EXT, VTHN, kStage, M32, NOTRUNC, PAIR>(qz, c, vtc, n_ev, k * kWave,
+                                                                         sk, vmin_l, vmax_l);
     } else {
-      conv_events<NIT, SAT, EXT, VTHN, kMask, M32, NOTRUNC>(qz, c, vtc, n_ev, k * kWave,
-                                                                  sk, vmin_l, vmax_l);
+      conv_events<NIT, SAT, EXT, VTHN, kMask, M32, NOTRUNC, PAIR>(qz, c, vtc, n_ev, k * kWave,
+                                                                        sk, vmin_l, vmax_l);
     }
     __syncthreads();
   }

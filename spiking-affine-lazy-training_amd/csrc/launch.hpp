@@ -10,11 +10,13 @@ namespace salt {
 
 constexpr int kLdsMax = 160 * 1024;  // gfx950 LDS per workgroup
 
-// Conv flags: bit 4 = no queue truncation possible (max_queue_len >= stream length),
-// bit 3 = candidate masks fit 32 bits, bit 2 = saturate, bit 1 = per-neuron extremes,
-// bit 0 = per-neuron thresholds.
-enum : int { kConvNoTrunc = 16, kConvM32 = 8, kConvSat = 4, kConvExt = 2, kConvVthN = 1 };
-constexpr int kConvFlagCombos = 32;
+// Conv flags: bit 5 = two events per step (needs bit 3), bit 4 = no queue truncation
+// possible (max_queue_len >= stream length), bit 3 = candidate masks fit 32 bits,
+// bit 2 = saturate, bit 1 = per-neuron extremes, bit 0 = per-neuron thresholds.
+enum : int {
+  kConvPair = 32, kConvNoTrunc = 16, kConvM32 = 8, kConvSat = 4, kConvExt = 2, kConvVthN = 1
+};
+constexpr int kConvFlagCombos = 64;
 
 // Iteration counts with an instantiated kernel family.
 #define SALT_CONV_NITS(X) X(1) X(2) X(3) X(4) X(8)

@@ -197,6 +197,7 @@ struct ConvPlan {
   int H, W, HW, NC, NC2, WPO, Gi, G, nit, ncg, nsb, Rw, R, n_rb, merge, spw;
   int Wp, VS, QS;  // LDS row stride and slot strides (choose_layout)
   int tsplit;      // no queue truncation possible: times and counts in separate arrays
+  int pair;        // two events per step, one per half-wave (NC2 <= 32)
   size_t lds;
 };
 
@@ -209,7 +210,8 @@ size_t conv_lds_bytes(const salt_layer_desc* d, const salt_qparams* p, const Con
                       bool ext) {
   const ConvLds l = conv_lds_layout(p->n_table, pl.spw, pl.ncg, pl.nsb, pl.nit * pl.Gi, pl.nit,
                                     pl.VS, pl.QS, pl.Rw * pl.Wp, ext,
-                                    p->v_th_kind == SALT_VTH_PER_NEURON, pl.tsplit != 0);
+                                    p->v_th_kind == SALT_VTH_PER_NEURON, pl.tsplit != 0,
+                                    pl.pair != 0);
   return (size_t)l.words * 4;
 }
 
@@ -275,12 +277,12 @@ double conv_access_cycles(ConvAccess which, int Gi, int NC, int S, int K, int Wp
 void choose_layout(const salt_layer_desc* d, const salt_qparams* p, bool ext, size_t budget,
                    ConvPlan* pl) {
   default_layout(d, pl);
-  const std::array<int, 17> key = {pl->W, pl->Rw, pl->Gi, pl->NC, d->s, d->k, d->ic, pl->nit,
+  const std::array<int, 18> key = {pl->W, pl->Rw, pl->Gi, pl->NC, d->s, d->k, d->ic, pl->nit,
                                    pl->ncg, pl->nsb, pl->spw, p->n_table, (int)ext,
-                                   p->v_th_kind == SALT_VTH_PER_NEURON, pl->tsplit,
+                                   p->v_th_kind == SALT_VTH_PER_NEURON, pl->tsplit, pl->pair,
                                    (int)(budget >> 4), (int)(budget & 15)};
   static std::mutex mu;
-  static std::map<std::array<int, 17>, std::array<int, 3>> cache;
+  static std::map<std::array<int, 18>, std::array<int, 3>> cache;
   {
     std::lock_guard<std::mutex> g(mu);
     auto it = cache.find(key);
@@ -343,6 +345,53 @@ bool plan_override(int* ncg_max, int* nsb) {
   return e && sscanf(e, "%d,%d", ncg_max, nsb) == 2 && *ncg_max >= 1 && *nsb >= 1;
 }
 
+// SALT_CONV_PAIR=0 / =1 forces steps of one / two events (where candidates fit half a
+// wave) for comparisons and tests; both give the same results.  -1: not forced.
+int pair_override() {
+  const char* e = getenv("SALT_CONV_PAIR");
+  if (!e || (e[0] != '0' && e[0] != '1')) return -1;
+  return e[0] - '0';
+}
+
+// Compute units of the current device (256 on MI355X, the fallback).
+int device_cus() {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> g(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n < 1)
+    n = 256;
+  cache[dev] = n;
+  return n;
+}
+
+int32_t plan_conv_mode(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext,
+                       bool notrunc, bool pair, ConvPlan* pl);
+
+// Chooses between steps of one event and steps of two (a half-wave each, for events
+// whose candidate blocks are disjoint; candidates must fit 32 lanes).  Pairs shorten a
+// stream's chain of steps by up to half -- 20% less time for the heaviest conv1 stream
+// of configuration 3 -- but, with as many waves per stream, do more work per event (the
+// steps with one event leave half a wave idle) and need more LDS; measured on MI355X
+// they win while the grid has fewer than two work-groups per compute unit (B <= 384 on
+// configuration 3) and lose when it fills the chip (B = 1024).
+int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext,
+                  bool notrunc, ConvPlan* pl) {
+  const int NC = (d->k - 1) / std::max(d->s, 1) + 1;
+  const int force = pair_override();
+  if (NC * NC <= kWave / 2 && force != 0) {
+    const int32_t rc = plan_conv_mode(d, p, B, ext, notrunc, true, pl);
+    if (rc) return rc;
+    if (force == 1 || (long)B * pl->n_rb < 2L * device_cus()) return 0;
+  }
+  return plan_conv_mode(d, p, B, ext, notrunc, false, pl);
+}
+
 // Chooses the partition of a conv layer.  One work-group per stream holds the whole
 // output plane whenever its LDS fits; its waves are channel groups, each with one
 // iteration per event where 8 waves suffice (a lone wave per SIMD is latency-bound,
@@ -350,8 +399,9 @@ bool plan_override(int* ncg_max, int* nsb) {
 // barriers; row sub-bands are supported but unbalanced for clustered events).
 // Otherwise several work-groups per stream each take a band of rows.
 // notrunc: max_queue_len >= the stream length, so no queue can be truncated.
-int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext,
-                  bool notrunc, ConvPlan* pl) {
+// pair: steps of two events (needs NC2 <= 32).
+int32_t plan_conv_mode(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext,
+                       bool notrunc, bool pair, ConvPlan* pl) {
   pl->tsplit = notrunc ? 1 : 0;
   pl->H = (d->h_in + 2 * d->p - d->k) / d->s + 1;
   pl->W = (d->w_in + 2 * d->p - d->k) / d->s + 1;
@@ -363,7 +413,8 @@ int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool e
     return fail(-3, "conv: %d candidate positions per event (k=%d, s=%d) exceed 64", pl->NC2,
                 d->k, d->s);
   pl->WPO = (pl->NC2 + 31) / 32;
-  pl->Gi = kWave / pl->NC2;
+  pl->pair = pair && pl->NC2 <= kWave / 2 ? 1 : 0;
+  pl->Gi = (pl->pair ? kWave / 2 : kWave) / pl->NC2;  // slots per (half-)wave
   const int H = pl->H, OC = d->oc;
   int ncg_max = kConvMaxWaves, nsb = 1;
   plan_override(&ncg_max, &nsb);
@@ -584,7 +635,8 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     const int flags = (sat ? kConvSat : 0) | (ext ? kConvExt : 0) |
                       (prm->v_th_kind == SALT_VTH_PER_NEURON ? kConvVthN : 0) |
                       (pl.NC2 <= 32 ? kConvM32 : 0) |
-                      (pl.tsplit ? kConvNoTrunc : 0);  // the layout follows this flag
+                      (pl.tsplit ? kConvNoTrunc : 0) |  // the layout follows these two
+                      (pl.pair ? kConvPair : 0);
     HIP_TRY(launch_conv(a, pl, flags, B, st));
     if (!pl.merge) {
       CompactArgs c;

@@ -128,6 +128,54 @@ def test_conv_streams_per_work_group_match_oracle(spw, monkeypatch):
         assert_layer_equal(out, ref, tag=f"spw {spw} {case}")
 
 
+def _clustered_sources(rng, B, L, ic, h, w, patch):
+    """Sources in a few patch x patch squares, visited in bursts, so that consecutive
+    events share, overlap or miss each other's candidate blocks in runs of every length."""
+    src = np.zeros((B, L), np.int32)
+    for b in range(B):
+        i = 0
+        while i < L:
+            n = int(rng.integers(1, 12))
+            y0, x0 = rng.integers(0, h - patch + 1), rng.integers(0, w - patch + 1)
+            y = y0 + rng.integers(0, patch, n)
+            x = x0 + rng.integers(0, patch, n)
+            c = rng.integers(0, ic, n)
+            src[b, i:i + n] = (c * h * w + y * w + x)[:L - i]
+            i += n
+    return src
+
+
+@pytest.mark.parametrize("pair", ["0", "1"])
+def test_conv_one_and_two_events_per_step_match_oracle(pair, monkeypatch):
+    """Steps of one event and of two (forced through SALT_CONV_PAIR): uniform and
+    clustered sources, whole-plane, sub-band and row-band plans, truncated and untruncated
+    queues give the oracle's streams, registers and extremes."""
+    monkeypatch.setenv("SALT_CONV_PAIR", pair)
+    cases = [((2, 34, 34, 16, 5, 2, 0, 6, 500), None, False), ((2, 34, 34, 16, 5, 2, 0, 6, 500), None, True),
+             ((16, 15, 15, 32, 3, 2, 0, 6, 400), None, True), ((2, 12, 12, 8, 3, 1, 1, 5, 300), "2,2", True),
+             ((1, 130, 130, 4, 3, 1, 0, 3, 600), None, True), ((3, 20, 20, 6, 4, 2, 1, 5, 300), None, False)]
+    for mi, (case, plan, clustered) in enumerate(cases):
+        ic, h, w, oc, k, s, p, B, L = case
+        if plan:
+            monkeypatch.setenv("SALT_CONV_PLAN", plan)
+        else:
+            monkeypatch.delenv("SALT_CONV_PLAN", raising=False)
+        rng = np.random.default_rng(700 + 10 * int(pair) + mi)
+        layer = ConvLayer(name="c", ic=ic, h_in=h, w_in=w, oc=oc, k=k, s=s, p=p, init_k=1.0,
+                          max_queue_len=int(rng.choice([L + 1, max(2, L // 25)])),
+                          max_out_spikes=4 * L * oc)
+        params, rm = _params(rng, layer.weight_shape, layer.n_neurons, oc, MODES[mi % 5], 8,
+                             ["scalar", "channel", "neuron"][mi % 3])
+        times, src, n_real = _events(rng, B, L, ic * h * w)
+        if clustered:
+            src = _clustered_sources(rng, B, L, ic, h, w, 2 * k)
+        print("pair", pair, "case", case, "plan", plan, "clustered", clustered, flush=True)
+        out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+        geom, prm, cap = oracle_spec(layer, params, rm)
+        ref = O.layer_forward(geom, prm, times, src, n_real, cap)
+        assert_layer_equal(out, ref, tag=f"pair {pair} {case} {plan} {clustered}")
+
+
 def test_without_neuron_extremes_same_streams_and_registers():
     rng = np.random.default_rng(5)
     layer = ConvLayer(name="c", ic=2, h_in=34, w_in=34, oc=16, k=5, s=2, p=0, init_k=1.0,
