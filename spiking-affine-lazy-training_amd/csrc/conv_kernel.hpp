@@ -24,10 +24,10 @@
 // (a broadcast).
 //
 // No lane predicates in the event loop.  A lane without an update this event (no
-// candidate, or a full queue) reads and writes its own spare words, which hold zeros:
-// a zero register and a zero code give U = 0 and never fire, and the extremes start at
-// 0.  Channel slots past a wave's channels likewise hold zero codes and an unreachable
-// threshold.
+// candidate, or a full queue) reads and writes spare words (registers zero, thresholds
+// unreachable) and a zero code: a zero register and a zero
+// code give U = 0 and never fire, and the extremes start at 0.  Channel slots past a
+// wave's channels likewise hold zero codes and an unreachable threshold.
 //
 // Output.  With the whole plane in the work-group, each wave stores the ballot of its
 // spikes per (chunk event, iteration) and its spike count per chunk event in LDS; after
@@ -86,9 +86,17 @@ struct ConvArgs {
   uint32_t* masks;
 };
 
-// Entries of the per-position (time, count) array: the band's PWs padded positions, then
-// one spare per lane.
-__host__ __device__ inline int conv_tcn(int PWs) { return PWs + kWave; }
+// Spare positions.  A lane without a candidate in an event reads and writes a spare
+// position of its own, which no event touches; every lane's address is then one base
+// (the event's position base, or the lane's spare base) plus its lane constant.  Bands
+// of at least NC rows (pad) keep the spares in padding columns: position (dy, W + dx) for
+// candidate offset (dy, dx), with rows of Wp >= W + NC; smaller bands keep NC2 spare
+// words after their PWs positions.
+__host__ __device__ inline bool conv_spare_pad(int Rw, int NC) { return Rw >= NC; }
+// Words of a per-position array (registers of a slot, (time, count) entries).
+__host__ __device__ inline int conv_pos_words(int PWs, int NC2, bool pad) {
+  return pad ? PWs : PWs + NC2;
+}
 
 // LDS layout of a conv_layer_kernel work-group, in 4-byte words: a shared part (decay
 // table, ballot-bit map, reduction slots, int32 weight codes per channel group), one
@@ -111,19 +119,19 @@ constexpr int kConvEvtBufs = 3;
 // step, or two (pair: the events of the step's two half-waves).
 __host__ __device__ inline int conv_recs(bool pair) { return (pair ? 2 : 1) * (kWave + 2); }
 
-// PWs: padded positions of a band (rows x Wp); vs >= PWs + NC2 and qs >= ICKK + 1: slot
-// strides (a slot's registers are followed by its NC2 spare words, its codes by a zero).
+// PWs: padded positions of a band (rows x Wp); npos = conv_pos_words(); vs >= npos and
+// qs >= ICKK + 1: slot strides (a slot's codes are followed by a zero).
 // tsplit (no queue truncation possible): the per-position entries are last-update times
 // alone, and the queue counts a separate array (kept by the decode, read at the end).
 // pair: two events per step (one per half-wave).
 __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg, int nsb,
                                                    int Gp, int nit, int vs, int qs, int PWs,
-                                                   bool ext, bool vthn, bool tsplit,
+                                                   int npos, bool ext, bool vthn, bool tsplit,
                                                    bool pair) {
   ConvLds l;
   l.vs = vs;
   l.qst = qs;
-  l.tcn = conv_tcn(PWs);
+  l.tcn = npos;
   int o = 0;
   l.ext = o;     o += n_table + 2;
   l.lanemap = o; o += 2 * kWave;  // int2 {slot, position offset} per ballot bit
@@ -178,13 +186,14 @@ struct ConvLane {
   uint64_t lm;          // this lane's candidate bit (0 for lanes without a slot)
   int rh;               // pair: the lane's record of a step (its half-wave), else 0
   int lp, lv, lq;       // position / register / code offsets relative to an event's bases
-  int v_spare, q_zero, tc_spare;  // this lane's spare register word, zero code, spare entry
+  int q_zero;           // this lane's zero code
   int GiVS, GiQS;
   int cand, oc_lane, mql, ntab;
   // byte offsets from the LDS base, for the event loop
   int extb;                     // decay table
   int lvb, lqb, ltb;            // register, code, (time, count) entry of an event's base
-  int v_spare_b, q_zero_b, tc_spare_b, tc_common_b;
+  int q_zero_b;
+  int sb;                       // spare base (records' units: position x 4)
   int GiVSb, GiQSb;             // per iteration
   int dmn, dmx, dth;            // register array -> extremes / per-neuron thresholds
 };
@@ -211,11 +220,11 @@ __device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, 
   const int slot_t = lane_on ? slot0 : 0;
   c.lm = lane_on ? (1ull << c.cand) : 0ull;
   c.lp = dy * g.Wp + dx;
-  c.lv = slot0 * VS + c.lp;
-  c.lq = slot0 * QS - dy * g.S * g.K - dx * g.S;
-  c.v_spare = slot_t * VS + PWs + c.cand;
+  // Lanes without a slot are never covered and use slot 0's spare words (VS >=
+  // conv_pos_words() keeps them inside slot 0's region).
+  c.lv = slot_t * VS + c.lp;
+  c.lq = slot_t * QS - dy * g.S * g.K - dx * g.S;
   c.q_zero = slot_t * QS + g.IC * g.K * g.K;
-  c.tc_spare = PWs + lane;
   c.GiVS = Gi * VS;
   c.GiQS = Gi * QS;
   c.oc_lane = oc0 + slot0;
@@ -227,12 +236,10 @@ __device__ __forceinline__ void conv_lane_setup(ConvLane& c, const ConvGeom& g, 
   c.lvb = b0 + (vw + c.lv) * 4;
   c.lqb = b0 + (qw + c.lq) * 4;
   c.ltb = b0 + tw * 4 + c.lp * tcb;
-  // Lanes without a candidate in the event read one common spare (time, count) entry (a
-  // broadcast, not a bank conflict); their writes go to per-lane spare words.
-  c.v_spare_b = b0 + (vw + c.v_spare) * 4;
   c.q_zero_b = b0 + (qw + c.q_zero) * 4;
-  c.tc_spare_b = b0 + tw * 4 + c.tc_spare * tcb;
-  c.tc_common_b = b0 + tw * 4 + PWs * tcb;
+  // spare position: (dy, W + dx) in the padding columns, or word PWs + cand
+  const int spare = conv_spare_pad(PWs / g.Wp, g.NC) ? g.W + c.lp : PWs + c.cand;
+  c.sb = (spare - c.lp) * 4;
   c.extb = (int)lds_addr(c.ext);
   c.GiVSb = c.GiVS * 4;
   c.GiQSb = c.GiQS * 4;
@@ -425,11 +432,15 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   // A position whose queue is full (max_queue_len real columns) drops the event and
   // its time (connectivity/conv.py:57-99 truncates the queue).
   auto act_of = [&](bool vc, const int2& st) { return NOTRUNC ? vc : (vc && st.y < c.mql); };
-  auto read_ops = [&](Ops& o, const int4& r, bool vc, const int2& st) {
+  // An event's base for this lane: the event's position base, or the spare base when
+  // the lane has no candidate (NOTRUNC: also its register base, as every candidate
+  // updates).
+  auto base_of = [&](const int4& r, bool vc) { return vc ? r.y : c.sb; };
+  auto read_ops = [&](Ops& o, const int4& r, int bse, bool vc, const int2& st) {
     const bool act = act_of(vc, st);
     // Decay code: dt = 0 -> identity, 1..n -> table, > n -> 0 (an unsigned clamp).
     o.A = lds_ld<int32_t>(c.extb + (int)(min((uint32_t)(r.x - st.x), nt1) << 2));
-    o.va = act ? r.y + c.lvb : c.v_spare_b;
+    o.va = (NOTRUNC ? bse : (act ? r.y : c.sb)) + c.lvb;
     o.qa = act ? r.z + c.lqb : c.q_zero_b;
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
@@ -448,24 +459,26 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   int4 r = c.rec[rh];
   int2 r1 = kRec1 ? c.rec1[rh] : make_int2(0, 0);
   bool vc = covers(r, r1);
-  int pab = (r.y << kTcShift) + c.ltb;  // this lane's (time, count) entry for the event
-  int2 st = tc_load(vc ? pab : c.tc_common_b);
+  int bse = base_of(r, vc);
+  int pab = (bse << kTcShift) + c.ltb;  // this lane's (time, count) entry for the event
+  int2 st = tc_load(pab);
   int4 rn = c.rec[RS + rh];  // records past the last step cover nothing
   int2 rn1 = kRec1 ? c.rec1[RS + rh] : make_int2(0, 0);
   Ops o;
-  read_ops(o, r, vc, st);
+  read_ops(o, r, bse, vc, st);
   // One event; everything carried becomes the next event's.
   auto event = [&](int e) {
     // this event's positions: time (and count), written by every lane of the position
     // (the slots of one candidate write the same entry with the same value)
     if (NOTRUNC)
-      lds_st<int32_t>(vc ? pab : c.tc_spare_b, r.x);
+      lds_st<int32_t>(pab, r.x);
     else
-      lds_st_tc(vc ? pab : c.tc_spare_b, act_of(vc, st) ? r.x : st.x, st.y + 1);
+      lds_st_tc(pab, act_of(vc, st) ? r.x : st.x, st.y + 1);
     // the next event's positions, after that write
     const bool vcn = covers(rn, rn1);
-    const int pabn = (rn.y << kTcShift) + c.ltb;
-    const int2 stn = tc_load(vcn ? pabn : c.tc_common_b);
+    const int bsen = base_of(rn, vcn);
+    const int pabn = (bsen << kTcShift) + c.ltb;
+    const int2 stn = tc_load(pabn);
     const int4 rn2 = c.rec[RS * (e + 2) + rh];
     const int2 rn12 = kRec1 ? c.rec1[RS * (e + 2) + rh] : make_int2(0, 0);
     asm volatile("" ::: "memory");  // the reads above go out before this event's update
@@ -487,7 +500,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
       bal[it] = __ballot(keep);
     }
     asm volatile("" ::: "memory");  // the next event's reads come after these writes
-    read_ops(o, rn, vcn, stn);
+    read_ops(o, rn, bsen, vcn, stn);
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       if (MODE == kStage) {
@@ -626,7 +639,8 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int ICKK = g.IC * g.K * g.K;
   const Quant& qz = a.qz;
   const ConvLds lay = conv_lds_layout(qz.n_table, a.spw, a.ncg, a.nsb, Gp, NIT, a.VS, a.QS,
-                                      PWs, EXT, VTHN, NOTRUNC, PAIR);
+                                      PWs, conv_pos_words(PWs, g.NC2, conv_spare_pad(a.Rw, g.NC)),
+                                      EXT, VTHN, NOTRUNC, PAIR);
   const int VS = lay.vs, QS = lay.qst;
   constexpr int RS = PAIR ? 2 : 1;  // records per step
   // regions: this (stream, sub-band)'s, the stream's sub-band 0's, this wave's, and the

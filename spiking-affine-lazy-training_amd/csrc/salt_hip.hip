@@ -208,17 +208,26 @@ int round_nit(int n) {  // smallest instantiated iteration count >= n
 
 size_t conv_lds_bytes(const salt_layer_desc* d, const salt_qparams* p, const ConvPlan& pl,
                       bool ext) {
+  const int pws = pl.Rw * pl.Wp;
   const ConvLds l = conv_lds_layout(p->n_table, pl.spw, pl.ncg, pl.nsb, pl.nit * pl.Gi, pl.nit,
-                                    pl.VS, pl.QS, pl.Rw * pl.Wp, ext,
+                                    pl.VS, pl.QS, pws,
+                                    conv_pos_words(pws, pl.NC2, conv_spare_pad(pl.Rw, pl.NC)),
+                                    ext,
                                     p->v_th_kind == SALT_VTH_PER_NEURON, pl.tsplit != 0,
                                     pl.pair != 0);
   return (size_t)l.words * 4;
 }
 
-// The plain layout: unpadded rows, the smallest odd slot strides.
+// The smallest row stride: bands of NC rows or more keep their spare positions in NC
+// padding columns.
+int min_row_stride(const ConvPlan* pl) {
+  return pl->W + (conv_spare_pad(pl->Rw, pl->NC) ? pl->NC : 0);
+}
+
+// The plain layout: the smallest row stride, the smallest odd slot strides.
 void default_layout(const salt_layer_desc* d, ConvPlan* pl) {
-  pl->Wp = pl->W;
-  pl->VS = (pl->Rw * pl->W + pl->NC2) | 1;
+  pl->Wp = min_row_stride(pl);
+  pl->VS = conv_pos_words(pl->Rw * pl->Wp, pl->NC2, conv_spare_pad(pl->Rw, pl->NC)) | 1;
   pl->QS = (d->ic * d->k * d->k + 1) | 1;
 }
 
@@ -269,8 +278,9 @@ double conv_access_cycles(ConvAccess which, int Gi, int NC, int S, int K, int Wp
   return sum / 32.0;
 }
 
-// Chooses the row stride Wp >= W and the slot strides VS, QS of a plan that minimise the
-// modelled bank-conflict cycles of the event loop's LDS accesses (register read + write,
+// Chooses the row stride Wp >= min_row_stride() and the slot strides VS, QS of a plan
+// that minimise the modelled bank-conflict cycles of the event loop's LDS accesses
+// (register read + write,
 // code read, (time, count) read + write; weights from the measured per-access costs),
 // within `budget` bytes of LDS per work-group.  Plans repeat for every call, so the
 // choice is cached.
@@ -301,11 +311,12 @@ void choose_layout(const salt_layer_desc* d, const salt_qparams* p, bool ext, si
   }
   ConvPlan best = *pl;
   double best_cost = 1e30;
-  for (int wp = pl->W; wp <= pl->W + 12; ++wp) {
-    const int pws = pl->Rw * wp;
+  const int wp0 = min_row_stride(pl);
+  for (int wp = wp0; wp <= wp0 + 12; ++wp) {
+    const int v0 = conv_pos_words(pl->Rw * wp, pl->NC2, conv_spare_pad(pl->Rw, pl->NC));
     int vs_best = 0;
     double v_best = 1e30;
-    for (int vs = pws + pl->NC2; vs < pws + pl->NC2 + 64; ++vs) {
+    for (int vs = v0; vs < v0 + 64; ++vs) {
       const double c = conv_access_cycles(kAccV, pl->Gi, pl->NC, d->s, d->k, wp, vs);
       if (c < v_best) { v_best = c; vs_best = vs; }
     }
