@@ -356,20 +356,6 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
   return n - __popcll(seconds);
 }
 
-// lo/hi of lane e <- the wave-uniform 64-bit value v; other lanes keep theirs.  M0 holds
-// the lane (written by a scalar move, which v_writelane may use at once); the value
-// comes straight from the compare's scalar result, so no scalar instruction waits for a
-// vector one.
-__device__ __forceinline__ void stage_to_lane(uint32_t& lo, uint32_t& hi, uint64_t v, int e) {
-  asm volatile(
-      "s_mov_b32 m0, %[e]\n\t"
-      "v_writelane_b32 %[lo], %[vlo], m0\n\t"
-      "v_writelane_b32 %[hi], %[vhi], m0"
-      : [lo] "+v"(lo), [hi] "+v"(hi)
-      : [e] "s"(e), [vlo] "s"((uint32_t)v), [vhi] "s"((uint32_t)(v >> 32))
-      : "m0");
-}
-
 // Where a wave's spikes go.
 enum ConvMode { kStage = 0, kMask = 1 };
 

@@ -10,6 +10,8 @@
 // (WLDS), else from global memory -- and is loaded one event ahead.
 #pragma once
 
+#include <type_traits>
+
 #include "salt_device.hpp"
 
 namespace salt {
@@ -46,92 +48,117 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
                                           int32_t (&mx)[NPL], const int32_t (&vth)[NPL],
                                           int& out_base) {
   const Quant& qz = a.qz;
-  const int fa = qz.fa, rc = qz.rc, fV = qz.fV;
+  const int fa = qz.fa, fV = qz.fV;
+  // The rounding constant in a VGPR for the whole loop: a VALU instruction reads one
+  // scalar operand here, and the decay multiply-add's is the event's decay code.
+  int rc = qz.rc;
+  asm volatile("" : "+v"(rc));
   const int lane = threadIdx.x;
-  // Lanes past the slice read a valid code of the slice (col is clamped) and are never
-  // reported; their threshold is unreachable.
-  auto column = [&](int s, int k) -> QT {
-    return WLDS ? wl[s * sw + col[k]] : qt[(size_t)s * a.n_out + n0 + col[k]];
-  };
-  // DIRECT: bit e & 31 of fired[h][k] (h = e / 32) records that this lane's neuron k
-  // fired at the chunk's event e -- vector operations only, so that the event loop has
-  // no branch on the compare -- and the chunk's spikes are appended after its events.
-  uint32_t fired[2][NPL];
+  // WLDS: lane e holds the LDS index of its event's weight row, multiplied out once per
+  // chunk, so that no scalar instruction waits for a v_readlane in the loop.
+  const int rowv = WLDS ? sv * sw : 0;
+  // An event's operands, fetched one event ahead: its decay code and, per neuron, its
+  // weight.  Lanes past the slice read a valid weight of the slice (col is clamped) and
+  // are never reported; their threshold is unreachable.
+  auto load = [&](QT (&q)[NPL], int& A, int e) {  // past the chunk: a harmless reload
+    const int ec = min(e, kWave - 1);
+    A = rdlane(Aj, ec);
+    if (WLDS) {
+      const int row = rdlane(rowv, ec);
 #pragma unroll
-  for (int k = 0; k < NPL; ++k) fired[0][k] = fired[1][k] = 0;
+      for (int k = 0; k < NPL; ++k) q[k] = wl[row + col[k]];
+    } else {
+      const int s_e = rdlane(sv, ec);
+#pragma unroll
+      for (int k = 0; k < NPL; ++k) q[k] = qt[(size_t)s_e * a.n_out + n0 + col[k]];
+    }
+  };
+  // DIRECT: lane e of klo/khi[k] collects event e's ballot of the neurons that kept their
+  // value (written by v_writelane from the compare's scalar result: no per-lane bit
+  // arithmetic in the loop); the chunk's spikes are placed after its events.
+  uint32_t klo[NPL], khi[NPL];
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) klo[k] = khi[k] = ~0u;
   // One event: process_event (salt_core/quant/scan.py:22-52) for every neuron, then its
-  // spikes (DIRECT: recorded in fired[h]; else the chunk's spike-mask words).
-  auto step = [&](int e, const QT (&qc)[NPL], uint32_t (&fh)[NPL]) {
-    const int A = rdlane(Aj, e);
+  // spikes.  LO: the slice has 32 neurons or fewer, so the ballot's low half holds them.
+  // FV0: f_V = 0, the weight is added unshifted.
+  auto step = [&](int e, const QT (&qc)[NPL], int A, auto lo_only, auto fv0) {
+    constexpr bool LO = decltype(lo_only)::value, FV0 = decltype(fv0)::value;
 #pragma unroll
     for (int k = 0; k < NPL; ++k) {
       const int32_t d = decay_mul<F24>(V[k], A, fa, rc);
-      const int32_t u = (int32_t)((uint32_t)d + ((uint32_t)(int32_t)qc[k] << fV));
+      const uint32_t qw = FV0 ? (uint32_t)(int32_t)qc[k] : ((uint32_t)(int32_t)qc[k] << fV);
+      const int32_t u = (int32_t)((uint32_t)d + qw);
       const int32_t f = fit_bits<SAT>(u, qz);
-      const bool fire = f >= vth[k];
-      V[k] = fire ? 0 : f;
+      const bool keep = f < vth[k];
+      V[k] = keep ? f : 0;
       mn[k] = min(mn[k], u);
       mx[k] = max(mx[k], u);
+      const uint64_t bal = __ballot(keep);
       if (DIRECT) {
-        fh[k] |= fire ? (1u << (e & 31)) : 0u;
+        if (LO) stage_to_lane_lo(klo[k], bal, e);
+        else stage_to_lane(klo[k], khi[k], bal, e);
       } else {
-        const uint64_t bal = __ballot(fire);
         const int w0 = (n0 + k * kWave) >> 5;
         if (lane < 2 && w0 + lane < a.words)
           a.masks[((size_t)b * a.L + base + e) * a.words + w0 + lane] =
-              lane ? (uint32_t)(bal >> 32) : (uint32_t)bal;
+              ~(lane ? (uint32_t)(bal >> 32) : (uint32_t)bal);
       }
     }
   };
-  auto load = [&](QT (&q)[NPL], int e) {  // past the chunk: a harmless reload
-    const int s_e = rdlane(sv, min(e, kWave - 1));
-#pragma unroll
-    for (int k = 0; k < NPL; ++k) q[k] = column(s_e, k);
-  };
-  // Two events per iteration with two column registers, each loaded one event before its
+  // Two events per iteration with two operand sets, each loaded one event before its
   // use: the loads' latency is covered by an event of arithmetic and no register has to
   // be copied or widened before its use (either would wait for the load).
   QT qa[NPL], qb[NPL];
-  load(qa, 0);
+  int Aa = 0, Ab = 0;
+  load(qa, Aa, 0);
   int e = 0;
-  // events [e, end) recording into fh; end is even unless it is ne
-  auto run = [&](int end, uint32_t (&fh)[NPL]) {
-    for (; e + 1 < end; e += 2) {
-      load(qb, e + 1);
-      step(e, qa, fh);
-      load(qa, e + 2);
-      step(e + 1, qb, fh);
+  auto run = [&](auto lo_only, auto fv0) {
+    for (; e + 1 < ne; e += 2) {
+      load(qb, Ab, e + 1);
+      step(e, qa, Aa, lo_only, fv0);
+      load(qa, Aa, e + 2);
+      step(e + 1, qb, Ab, lo_only, fv0);
     }
-    if (e < end) step(e++, qa, fh);
+    if (e < ne) step(e++, qa, Aa, lo_only, fv0);
   };
-  run(min(ne, 32), fired[0]);
-  run(ne, fired[1]);
+  const bool lo = DIRECT && NPL == 1 && sw <= 32;
+  if (fV == 0) {
+    if (lo) run(std::true_type{}, std::true_type{});
+    else run(std::false_type{}, std::true_type{});
+  } else {
+    if (lo) run(std::true_type{}, std::false_type{});
+    else run(std::false_type{}, std::false_type{});
+  }
   if (DIRECT) {
-    uint32_t any = 0;
+    // Lane = the chunk's event: its spikes (neurons ascending) follow those of the
+    // chunk's earlier events -- the (event, neuron) order of salt_core/stream.py.
+    uint64_t sp[NPL];
+    int cnt = 0;
 #pragma unroll
-    for (int k = 0; k < NPL; ++k) any |= fired[0][k] | fired[1][k];
-    if (__builtin_expect(__ballot(any != 0) != 0, 0)) {  // readout layers rarely fire
-      // (event, neuron) order: per event, the slice's neurons in ascending order
-      for (int e2 = 0; e2 < ne; ++e2) {
-        const int h = e2 >> 5, sh = e2 & 31;
-        // read with every lane active: a lane's VGPR value is only kept for the lanes
-        // that use it, so a read of another lane inside the branch below may see a reuse
-        const float te = (float)rdlane(tv, e2);
+    for (int k = 0; k < NPL; ++k) {
+      sp[k] = ~(((uint64_t)khi[k] << 32) | klo[k]);
+      cnt += __popcll(sp[k]);
+    }
+    if (__builtin_expect(__ballot(cnt != 0) != 0, 0)) {  // readout layers rarely fire
+      const int incl = wave_incl_scan(cnt);
+      const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+      int pos = out_base + incl - cnt;
+      const float te = (float)tv;  // this lane's event time
 #pragma unroll
-        for (int k = 0; k < NPL; ++k) {
-          const bool f = ((h ? fired[1][k] : fired[0][k]) >> sh) & 1u;
-          const uint64_t bal = __ballot(f);
-          if (bal == 0) continue;
-          if (f) {
-            const int idx = out_base + lanes_below(bal);
-            if (idx < a.cap) {
-              a.out_t[(size_t)b * a.cap + idx] = te;
-              a.out_s[(size_t)b * a.cap + idx] = n0 + k * kWave + lane;
-            }
+      for (int k = 0; k < NPL; ++k) {
+        uint64_t bits = sp[k];
+        while (bits) {
+          const int kb = __builtin_ctzll(bits);
+          bits &= bits - 1;
+          if (pos < a.cap) {
+            a.out_t[(size_t)b * a.cap + pos] = te;
+            a.out_s[(size_t)b * a.cap + pos] = n0 + k * kWave + kb;
           }
-          out_base += __popcll(bal);
+          ++pos;
         }
       }
+      out_base += total;
     }
   }
 }

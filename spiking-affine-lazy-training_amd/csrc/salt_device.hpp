@@ -108,6 +108,29 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
                                         __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// lo/hi of lane e <- the wave-uniform 64-bit value v; other lanes keep theirs.  M0 holds
+// the lane (written by a scalar move, which v_writelane may use at once); the value
+// comes straight from the compare's scalar result, so no scalar instruction waits for a
+// vector one.  (M0 is otherwise unused by the kernels that call this.)
+__device__ __forceinline__ void stage_to_lane(uint32_t& lo, uint32_t& hi, uint64_t v, int e) {
+  asm volatile(
+      "s_mov_b32 m0, %[e]\n\t"
+      "v_writelane_b32 %[lo], %[vlo], m0\n\t"
+      "v_writelane_b32 %[hi], %[vhi], m0"
+      : [lo] "+v"(lo), [hi] "+v"(hi)
+      : [e] "s"(e), [vlo] "s"((uint32_t)v), [vhi] "s"((uint32_t)(v >> 32))
+      : "m0");
+}
+// The low half alone (slices of 32 neurons or fewer).
+__device__ __forceinline__ void stage_to_lane_lo(uint32_t& lo, uint64_t v, int e) {
+  asm volatile(
+      "s_mov_b32 m0, %[e]\n\t"
+      "v_writelane_b32 %[lo], %[vlo], m0"
+      : [lo] "+v"(lo)
+      : [e] "s"(e), [vlo] "s"((uint32_t)v)
+      : "m0");
+}
+
 __device__ __forceinline__ int rdlane(int v, int lane) {
   return __builtin_amdgcn_readlane(v, lane);
 }
