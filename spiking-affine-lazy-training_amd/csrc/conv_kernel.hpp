@@ -53,6 +53,7 @@ constexpr int kConvBlockWaves = 16;  // waves per work-group (streams x waves pe
 struct ConvGeom {
   int IC, Win, HWin, OC, K, S, P, H, W, HW, NC, NC2, mql;
   int Wp;  // row stride of the per-position arrays in LDS (>= W)
+  float rHWin, rWin, rS;  // 1/HWin, 1/Win, 1/S (for div_small)
 };
 
 struct ConvArgs {
@@ -284,20 +285,35 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
                                            int sv, int j, int n_eff, int r0, int rn, int& oy0,
                                            int& ox0, int32_t* cnt) {
   const bool real = j < n_eff && sv >= 0;
-  int ch = 0, y = 0, x = 0;
-  if (real) {
-    ch = sv / g.HWin;
-    const int rem = sv - ch * g.HWin;
+  // source -> (channel, row, column); a source past the input is clamped into it (memory
+  // safety only: the host rejects such ids)
+  const int n_src = g.IC * g.HWin;
+  const int s = real ? min(sv, n_src - 1) : 0;
+  // Candidate output rows [ceil((y+P-K+1)/S), floor((y+P)/S)] within [r0, r0+rn) and
+  // columns within [0, W) (connectivity/conv.py:15-29); ceil((a+1)/S) = floor((a+S)/S),
+  // taken as floor((a+S+K*S)/S) - K to divide a non-negative number.
+  int ch, y, x, yhi, xhi;
+  if (n_src <= (1 << 22)) {  // every operand below 2^22: div_small
+    ch = div_small(s, g.HWin, g.rHWin);
+    const int rem = s - ch * g.HWin;
+    y = div_small(rem, g.Win, g.rWin);
+    x = rem - y * g.Win;
+    oy0 = div_small(y + g.P - g.K + g.S + g.K * g.S, g.S, g.rS) - g.K;
+    ox0 = div_small(x + g.P - g.K + g.S + g.K * g.S, g.S, g.rS) - g.K;
+    yhi = div_small(y + g.P, g.S, g.rS);
+    xhi = div_small(x + g.P, g.S, g.rS);
+  } else {
+    ch = s / g.HWin;
+    const int rem = s - ch * g.HWin;
     y = rem / g.Win;
     x = rem - y * g.Win;
-    ch = min(ch, g.IC - 1);  // memory safety only; the host rejects such ids
+    oy0 = floordiv_pos(y + g.P - g.K + g.S, g.S);
+    ox0 = floordiv_pos(x + g.P - g.K + g.S, g.S);
+    yhi = (y + g.P) / g.S;
+    xhi = (x + g.P) / g.S;
   }
-  // Candidate output rows [ceil((y+P-K+1)/S), floor((y+P)/S)] within [r0, r0+rn) and
-  // columns within [0, W) (connectivity/conv.py:15-29).
-  oy0 = floordiv_pos(y + g.P - g.K + g.S, g.S);
-  ox0 = floordiv_pos(x + g.P - g.K + g.S, g.S);
-  const int dyA = max(oy0, r0) - oy0, dyB = min((y + g.P) / g.S, r0 + rn - 1) - oy0;
-  const int dxA = max(ox0, 0) - ox0, dxB = min((x + g.P) / g.S, g.W - 1) - ox0;
+  const int dyA = max(oy0, r0) - oy0, dyB = min(yhi, r0 + rn - 1) - oy0;
+  const int dxA = max(ox0, 0) - ox0, dxB = min(xhi, g.W - 1) - ox0;
   const bool rel = real && dyA <= dyB && dxA <= dxB;
   uint64_t m = 0;
   if (rel) {
@@ -765,11 +781,12 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   auto walk = [&](int k) {
     const int bf = k & 1;
     int tot = 0, before = 0;
-    for (int w = 0; w < nwps; ++w) {
-      const int cw = swave0[w * lay.wave_words + lay.wcnt + bf * kWave + lane];
-      tot += cw;
-      before += (w % a.ncg < cg) ? cw : 0;
-    }
+    for (int s2 = 0; s2 < a.nsb; ++s2)  // wave s2 * ncg + g2: sub-band s2, channel group g2
+      for (int g2 = 0; g2 < a.ncg; ++g2) {
+        const int cw = swave0[(s2 * a.ncg + g2) * lay.wave_words + lay.wcnt + bf * kWave + lane];
+        tot += cw;
+        before += g2 < cg ? cw : 0;
+      }
     if (__ballot(tot != 0) == 0) return;  // no spike in the chunk
     const int incl = wave_incl_scan(tot);
     const int total = __builtin_amdgcn_readlane(incl, kWave - 1);

@@ -79,6 +79,18 @@ __device__ __forceinline__ int floordiv_pos(int a, int s) {  // s > 0
   return a >= 0 ? a / s : -((-a + s - 1) / s);
 }
 
+// n / d for 0 <= n < 2^22 and d >= 1, with rcp = 1 / d as float (within one ulp): the
+// float product is within one of n / d, so its truncation is the quotient or one off,
+// and one integer correction either way makes it exact.  A few instructions against a
+// generic 32-bit division's two dozen.
+__device__ __forceinline__ int div_small(int n, int d, float rcp) {
+  int q = (int)((float)n * rcp);
+  const int r = n - q * d;
+  q += r >= d ? 1 : 0;
+  q -= r < 0 ? 1 : 0;
+  return q;
+}
+
 __device__ __forceinline__ int wave_min(int v) {
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
   return v;

@@ -559,6 +559,9 @@ ConvGeom conv_geom(const salt_layer_desc* d, const ConvPlan& pl) {
   g.K = d->k; g.S = d->s; g.P = d->p; g.H = pl.H; g.W = pl.W; g.HW = pl.HW;
   g.NC = pl.NC; g.NC2 = pl.NC2; g.mql = d->max_queue_len;
   g.Wp = pl.Wp;
+  g.rHWin = 1.0f / (float)g.HWin;  // correctly rounded on the host
+  g.rWin = 1.0f / (float)g.Win;
+  g.rS = 1.0f / (float)g.S;
   return g;
 }
 
