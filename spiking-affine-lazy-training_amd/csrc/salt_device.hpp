@@ -83,7 +83,7 @@ __device__ __forceinline__ int floordiv_pos(int a, int s) {  // s > 0
 // float product is within one of n / d, so its truncation is the quotient or one off,
 // and one integer correction either way makes it exact.  A few instructions against a
 // generic 32-bit division's two dozen.
-__device__ __forceinline__ int div_small(int n, int d, float rcp) {
+__host__ __device__ inline int div_small(int n, int d, float rcp) {
   int q = (int)((float)n * rcp);
   const int r = n - q * d;
   q += r >= d ? 1 : 0;
