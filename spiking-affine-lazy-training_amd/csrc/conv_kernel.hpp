@@ -640,9 +640,9 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int W = g.W, Wp = g.Wp, PWs = a.Rw * Wp, PW = rn * W;
   const int ICKK = g.IC * g.K * g.K;
   const Quant& qz = a.qz;
+  const int npos = conv_pos_words(PWs, g.NC2, conv_spare_pad(a.Rw, g.NC));
   const ConvLds lay = conv_lds_layout(qz.n_table, a.spw, a.ncg, a.nsb, Gp, NIT, a.VS, a.QS,
-                                      PWs, conv_pos_words(PWs, g.NC2, conv_spare_pad(a.Rw, g.NC)),
-                                      EXT, VTHN, NOTRUNC, PAIR);
+                                      PWs, npos, EXT, VTHN, NOTRUNC, PAIR);
   const int VS = lay.vs, QS = lay.qst;
   constexpr int RS = PAIR ? 2 : 1;  // records per step
   // regions: this (stream, sub-band)'s, the stream's sub-band 0's, this wave's, and the
