@@ -503,10 +503,15 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     }
     asm volatile("" ::: "memory");  // the next event's reads come after these writes
     read_ops(o, rn, bsen, vcn, stn);
+    // The ballots are staged here, after the next event's reads have gone out: the
+    // lane index passes through an empty asm so that the compiler keeps the writes here
+    // (issued earlier, they would wait for the compare).
+    int el = e;
+    asm volatile("" : "+s"(el));
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       if (MODE == kStage) {
-        stage_to_lane(sg_lo[it], sg_hi[it], bal[it], e);
+        stage_to_lane(sg_lo[it], sg_hi[it], bal[it], el);
       } else if (!((bal[it] >> lane) & 1)) {
         // Bit = candidate index in the event's NC x NC grid (compaction decodes it).
         const size_t w = ((size_t)sk.b * sk.L + r1.y) * (size_t)(sk.OC * sk.WPO) +

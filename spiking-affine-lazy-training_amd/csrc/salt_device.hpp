@@ -120,27 +120,22 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
                                         __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// lo/hi of lane e <- the wave-uniform 64-bit value v; other lanes keep theirs.  M0 holds
-// the lane (written by a scalar move, which v_writelane may use at once); the value
-// comes straight from the compare's scalar result, so no scalar instruction waits for a
-// vector one.  (M0 is otherwise unused by the kernels that call this.)
+// v_writelane, which this compiler exposes as an LLVM intrinsic but not as a builtin:
+// lane `lane` of the result <- the wave-uniform `v`, other lanes <- `old`.  (The compiler
+// puts the lane select in M0, since a VALU instruction reads one scalar operand here.)
+extern "C" __device__ int salt_writelane_i32(int v, int lane, int old) __asm(
+    "llvm.amdgcn.writelane.i32");
+
+// lo/hi of lane e <- the wave-uniform 64-bit value v; other lanes keep theirs.  The value
+// comes straight from the compare's scalar result and the lane from the scalar loop
+// counter, so no scalar instruction waits for a vector one.
 __device__ __forceinline__ void stage_to_lane(uint32_t& lo, uint32_t& hi, uint64_t v, int e) {
-  asm volatile(
-      "s_mov_b32 m0, %[e]\n\t"
-      "v_writelane_b32 %[lo], %[vlo], m0\n\t"
-      "v_writelane_b32 %[hi], %[vhi], m0"
-      : [lo] "+v"(lo), [hi] "+v"(hi)
-      : [e] "s"(e), [vlo] "s"((uint32_t)v), [vhi] "s"((uint32_t)(v >> 32))
-      : "m0");
+  lo = (uint32_t)salt_writelane_i32((int)(uint32_t)v, e, (int)lo);
+  hi = (uint32_t)salt_writelane_i32((int)(uint32_t)(v >> 32), e, (int)hi);
 }
 // The low half alone (slices of 32 neurons or fewer).
 __device__ __forceinline__ void stage_to_lane_lo(uint32_t& lo, uint64_t v, int e) {
-  asm volatile(
-      "s_mov_b32 m0, %[e]\n\t"
-      "v_writelane_b32 %[lo], %[vlo], m0"
-      : [lo] "+v"(lo)
-      : [e] "s"(e), [vlo] "s"((uint32_t)v)
-      : "m0");
+  lo = (uint32_t)salt_writelane_i32((int)(uint32_t)v, e, (int)lo);
 }
 
 __device__ __forceinline__ int rdlane(int v, int lane) {
