@@ -272,10 +272,11 @@ __device__ __forceinline__ void lds_st_tc(int addr, int t, int cnt) {
 // source sv, index j; real when j < n_eff and sv >= 0), against the rows [r0, r0+rn):
 // records {time, position base * 4, code base * 4, candidate mask low} + {mask high,
 // event index} for the events with a candidate there, compacted in order, followed by
-// records with no candidate (mask 0) for the other lanes; with the permanent one at
-// index kWave, the record after a chunk's last event covers nothing, so the event loop
-// reads one record ahead without a bounds test.  Returns the number of events with a
-// candidate; oy0/ox0 = the event's first candidate row and column.
+// records with no candidate (mask 0) for the other lanes; with the two permanent ones
+// at indices kWave and kWave + 1, the two records after a chunk's last event cover
+// nothing, so the event loop reads two records ahead without a bounds test.  Returns
+// the number of events with a candidate; oy0/ox0 = the event's first candidate row and
+// column.
 // cnt (queue counts of a wave that keeps them, else null): each event adds one to the
 // count of every candidate position it has.
 // PAIR: the records go to steps of two events instead, and the number of steps is
