@@ -533,24 +533,29 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
   // 3 to 0 over each quarter of the chunk: the waves of other streams sharing a SIMD are
   // at other points of their chunks, so the one furthest behind in its own chunk is
   // served first instead of the oldest wave, which would otherwise run ahead and leave
-  // the younger ones to finish alone, latency-bound, at the end of the kernel.
+  // the younger ones to finish alone, latency-bound, at the end of the kernel.  PAIR
+  // (chosen for grids under two work-groups per CU, where a SIMD has few waves to order)
+  // keeps one priority: the steps cost more than they save there (measured).
+  constexpr int kSegs = PAIR ? 1 : 4;
   int e = 0;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    switch (q) {
-      case 0: __builtin_amdgcn_s_setprio(3); break;
-      case 1: __builtin_amdgcn_s_setprio(2); break;
-      case 2: __builtin_amdgcn_s_setprio(1); break;
-      default: __builtin_amdgcn_s_setprio(0); break;
+  for (int q = 0; q < kSegs; ++q) {
+    if (!PAIR) {
+      switch (q) {
+        case 0: __builtin_amdgcn_s_setprio(3); break;
+        case 1: __builtin_amdgcn_s_setprio(2); break;
+        case 2: __builtin_amdgcn_s_setprio(1); break;
+        default: __builtin_amdgcn_s_setprio(0); break;
+      }
     }
-    const int end = min(n_ev, (q + 1) * (kWave / 4));
+    const int end = min(n_ev, (q + 1) * (kWave / kSegs));
     for (; e + 1 < end; e += 2) {
       event(e);
       event(e + 1);
     }
     if (e < end) event(e++);
   }
-  __builtin_amdgcn_s_setprio(3);
+  if (!PAIR) __builtin_amdgcn_s_setprio(3);
   if (PAIR && MODE == kStage && lane < n_ev) {
     // step lane: half-wave h's ballot bits belong to the event of record 2 * lane + h
     const int j0 = c.rec1[2 * lane].y - base, j1 = c.rec1[2 * lane + 1].y;
