@@ -176,6 +176,30 @@ def test_conv_one_and_two_events_per_step_match_oracle(pair, monkeypatch):
         assert_layer_equal(out, ref, tag=f"pair {pair} {case} {plan} {clustered}")
 
 
+@pytest.mark.parametrize("pair", ["0", "1"])
+def test_conv_many_iterations_per_step_match_oracle(pair, monkeypatch):
+    """One channel group per stream (SALT_CONV_PLAN=1,1) puts every channel in one wave:
+    3 iterations per event for conv1's geometry (8 with two-event steps) and 2 for
+    conv2's (4 with two-event steps), clustered sources."""
+    monkeypatch.setenv("SALT_CONV_PAIR", pair)
+    monkeypatch.setenv("SALT_CONV_PLAN", "1,1")
+    for mi, case in enumerate([(2, 34, 34, 16, 5, 2, 0, 5, 400), (16, 15, 15, 32, 3, 2, 0, 5, 400)]):
+        ic, h, w, oc, k, s, p, B, L = case
+        rng = np.random.default_rng(1100 + 10 * int(pair) + mi)
+        layer = ConvLayer(name="c", ic=ic, h_in=h, w_in=w, oc=oc, k=k, s=s, p=p, init_k=1.0,
+                          max_queue_len=int(rng.choice([L + 1, max(2, L // 25)])),
+                          max_out_spikes=4 * L * oc)
+        params, rm = _params(rng, layer.weight_shape, layer.n_neurons, oc, MODES[2 * mi], 8,
+                             ["neuron", "channel"][mi])
+        times, src, n_real = _events(rng, B, L, ic * h * w)
+        src = _clustered_sources(rng, B, L, ic, h, w, 2 * k)
+        print("iterations pair", pair, "case", case, flush=True)
+        out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+        geom, prm, cap = oracle_spec(layer, params, rm)
+        ref = O.layer_forward(geom, prm, times, src, n_real, cap)
+        assert_layer_equal(out, ref, tag=f"iterations pair {pair} {case}")
+
+
 def test_without_neuron_extremes_same_streams_and_registers():
     rng = np.random.default_rng(5)
     layer = ConvLayer(name="c", ic=2, h_in=34, w_in=34, oc=16, k=5, s=2, p=0, init_k=1.0,
