@@ -77,19 +77,54 @@ struct CompactArgs {
   int32_t* out_n;
 };
 
-// Spike bitmasks -> ordered stream.  One wave per stream; lane = event within a chunk
-// of 64.  Words are in neuron order and bits within a word too, so walking them gives
-// the (event, neuron) order of salt_core/stream.py:24-46.
-__global__ void __launch_bounds__(64) compact_kernel(CompactArgs a) {
+// Spike bitmasks -> ordered stream, in segments of kCompactSeg events so that a stream's
+// walk and its padding spread over many waves: compact_count_kernel sums each segment's
+// spikes, compact_kernel (one wave per segment) starts its part of the stream after the
+// earlier segments' spikes.  Words are in neuron order and bits within a word too, so
+// walking them gives the (event, neuron) order of salt_core/stream.py:24-46.
+constexpr int kCompactSeg = 2048;
+
+int compact_segments(int L) { return std::max(1, (L + kCompactSeg - 1) / kCompactSeg); }
+
+// Spikes per (stream, segment): the segment's mask words as one flat, coalesced array.
+__global__ void __launch_bounds__(64) compact_count_kernel(CompactArgs a, int32_t* seg_cnt,
+                                                           int nseg) {
   const int lane = threadIdx.x;
-  const int b = blockIdx.x;
+  const int s = blockIdx.x, b = blockIdx.y;
   const int L = a.L;
   const int nr = a.n_real[b];
   const int n_eff = nr < 0 ? 0 : (nr < L ? nr : L);
-  int out_base = 0;
-  for (int base = 0; base < n_eff; base += kWave) {
+  const int j0 = min(n_eff, s * kCompactSeg), j1 = min(n_eff, j0 + kCompactSeg);
+  const uint32_t* m = a.masks + ((size_t)b * L + j0) * a.words;
+  const size_t nw = (size_t)(j1 - j0) * a.words;
+  int cnt = 0;
+  for (size_t i = lane; i < nw; i += kWave) cnt += __popc(m[i]);
+  const int total = __builtin_amdgcn_readlane(wave_incl_scan(cnt), kWave - 1);
+  if (lane == 0) seg_cnt[b * nseg + s] = total;
+}
+
+// One wave per (segment, stream); lane = event within a chunk of 64.
+__global__ void __launch_bounds__(64) compact_kernel(CompactArgs a, const int32_t* seg_cnt,
+                                                     int nseg) {
+  const int lane = threadIdx.x;
+  const int s = blockIdx.x, b = blockIdx.y;
+  const int L = a.L;
+  const int nr = a.n_real[b];
+  const int n_eff = nr < 0 ? 0 : (nr < L ? nr : L);
+  // this segment's first place in the stream, and the stream's spike count
+  int before = 0, all = 0;
+  for (int t = lane; t < nseg; t += kWave) {
+    const int c = seg_cnt[b * nseg + t];
+    before += t < s ? c : 0;
+    all += c;
+  }
+  before = __builtin_amdgcn_readlane(wave_incl_scan(before), kWave - 1);
+  all = __builtin_amdgcn_readlane(wave_incl_scan(all), kWave - 1);
+  int out_base = before;
+  const int j_end = min(n_eff, (s + 1) * kCompactSeg);
+  for (int base = s * kCompactSeg; base < j_end; base += kWave) {
     const int j = base + lane;
-    const bool ok = j < n_eff;
+    const bool ok = j < j_end;
     const uint32_t* m = a.masks + ((size_t)b * L + j) * a.words;
     int count = 0;
     if (ok)
@@ -132,9 +167,9 @@ __global__ void __launch_bounds__(64) compact_kernel(CompactArgs a) {
     }
     out_base += total;
   }
-  if (lane == 0) a.out_n[b] = out_base;
-  if (a.fill_pads)
-    for (int i = min(out_base, a.cap) + lane; i < a.cap; i += kWave) {
+  if (s == nseg - 1 && lane == 0) a.out_n[b] = all;
+  if (a.fill_pads)  // the segments share the padding
+    for (int i = min(all, a.cap) + s * kWave + lane; i < a.cap; i += nseg * kWave) {
       a.out_t[(size_t)b * a.cap + i] = kPadTime;
       a.out_s[(size_t)b * a.cap + i] = 0;
     }
@@ -565,11 +600,34 @@ ConvGeom conv_geom(const salt_layer_desc* d, const ConvPlan& pl) {
   return g;
 }
 
-size_t mask_bytes_conv(const ConvPlan& pl, const salt_layer_desc* d, int B, int L) {
-  return pl.merge ? 0 : (size_t)B * L * d->oc * pl.WPO * 4;
+// Workspace of a compacted layer: the spike masks, then (256-byte aligned) the spikes per
+// (stream, segment) of the compaction.
+size_t masks_end(size_t mask_bytes) { return (mask_bytes + 255) & ~(size_t)255; }
+size_t compact_bytes(size_t mask_bytes, int B, int L) {
+  return masks_end(mask_bytes) + (size_t)B * compact_segments(L) * 4;
 }
+size_t mask_only_conv(const ConvPlan& pl, const salt_layer_desc* d, int B, int L) {
+  return (size_t)B * L * d->oc * pl.WPO * 4;
+}
+size_t mask_bytes_conv(const ConvPlan& pl, const salt_layer_desc* d, int B, int L) {
+  return pl.merge ? 0 : compact_bytes(mask_only_conv(pl, d, B, L), B, L);
+}
+size_t mask_only_fc(const FcPlan& pl, int B, int L) { return (size_t)B * L * pl.words * 4; }
 size_t mask_bytes_fc(const FcPlan& pl, int B, int L) {
-  return pl.direct ? 0 : (size_t)B * L * pl.words * 4;
+  return pl.direct ? 0 : compact_bytes(mask_only_fc(pl, B, L), B, L);
+}
+
+// Launches the two compaction kernels over a layer's spike masks.
+int32_t launch_compact(const CompactArgs& c, int B, int L, size_t mask_bytes, void* ws,
+                       hipStream_t st) {
+  const int nseg = compact_segments(L);
+  int32_t* const seg = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + masks_end(mask_bytes));
+  const dim3 grid(nseg, B);
+  hipLaunchKernelGGL(compact_count_kernel, grid, dim3(kWave), 0, st, c, seg, nseg);
+  HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL(compact_kernel, grid, dim3(kWave), 0, st, c, (const int32_t*)seg, nseg);
+  HIP_TRY(hipGetLastError());
+  return 0;
 }
 
 int32_t fill(int32_t* p, int32_t v, size_t n, hipStream_t st) {
@@ -644,7 +702,9 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     a.masks = static_cast<uint32_t*>(d_workspace);
     if (!pl.merge) {
       if ((rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
-      if ((rc = fill(reinterpret_cast<int32_t*>(a.masks), 0, need / 4, st))) return rc;
+      if ((rc = fill(reinterpret_cast<int32_t*>(a.masks), 0,
+                     mask_only_conv(pl, desc, B, L) / 4, st)))
+        return rc;
     }
     const int flags = (sat ? kConvSat : 0) | (ext ? kConvExt : 0) |
                       (prm->v_th_kind == SALT_VTH_PER_NEURON ? kConvVthN : 0) |
@@ -660,8 +720,8 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
       c.n_real = in->d_n_real; c.masks = a.masks; c.cap = out->cap;
       c.fill_pads = out->fill_pads; c.out_t = out->d_times; c.out_s = out->d_src;
       c.out_n = out->d_n;
-      hipLaunchKernelGGL(compact_kernel, dim3(B), dim3(kWave), 0, st, c);
-      HIP_TRY(hipGetLastError());
+      if ((rc = launch_compact(c, B, L, mask_only_conv(pl, desc, B, L), d_workspace, st)))
+        return rc;
     }
     return 0;
   }
@@ -702,8 +762,7 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     c.n_real = in->d_n_real; c.masks = a.masks; c.cap = out->cap;
     c.fill_pads = out->fill_pads; c.out_t = out->d_times; c.out_s = out->d_src;
     c.out_n = out->d_n;
-    hipLaunchKernelGGL(compact_kernel, dim3(B), dim3(kWave), 0, st, c);
-    HIP_TRY(hipGetLastError());
+    if ((rc = launch_compact(c, B, L, mask_only_fc(pl, B, L), d_workspace, st))) return rc;
   }
   return 0;
 }
