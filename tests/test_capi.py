@@ -54,7 +54,9 @@ def test_workspace_size_is_host_only():
     d.max_queue_len, d.max_out_spikes = 100, 16
     rc = _lib.lib().salt_layer_workspace_size(ctypes.byref(d), ctypes.byref(_qp()), 64, 1000, 0,
                                              ctypes.byref(size))
-    assert rc == 0 and size.value == 64 * 1000 * 32 * 4  # partitioned: per-event spike masks
+    # partitioned: per-event spike masks, then one spike count per (stream, 2048-event
+    # compaction segment)
+    assert rc == 0 and size.value == 64 * 1000 * 32 * 4 + 64 * 1 * 4
 
 
 @pytest.mark.parametrize("kw", [dict(f_a=16), dict(i_V=31), dict(q_bits=12), dict(n_table=0),
