@@ -64,6 +64,13 @@ struct ConvArgs {
   int G, Gi, ncg, nsb, Rw, R;
   // spw streams per work-group (whole-plane plans), B streams in all
   int spw, B;
+  // Row-band plans: the events whose candidate rows meet each (stream, band), as original
+  // indices in order -- band (b, x) has bcnt[b * gridDim.x + x] of them from
+  // blist + b * bcap + boff[b * gridDim.x + x].  Null: every work-group reads its stream.
+  const int32_t* blist;
+  const int32_t* bcnt;
+  const int32_t* boff;
+  int bcap;
   int VS, QS;  // slot strides of the registers and the weight codes in LDS
   // quantisation
   Quant qz;
@@ -743,11 +750,24 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     return nr < 0 ? 0 : (nr < L ? nr : L);
   };
   const int n_eff = real_count(b);
-  // The chunk loop runs to the work-group's longest stream, so that every wave meets
-  // every barrier; a stream's chunks past its own events decode to no events.
+  // Row-band plans with event lists: this work-group's events are its list's entries.
+  const int32_t* lst = nullptr;
+  int n_list = 0;
+  if (a.blist && live) {
+    const int bi = b * gridDim.x + blockIdx.x;
+    n_list = __builtin_amdgcn_readfirstlane(a.bcnt[bi]);
+    lst = a.blist + (size_t)b * a.bcap + a.boff[bi];
+  }
+  // The chunk loop runs to the work-group's longest stream (or list), so that every wave
+  // meets every barrier; a stream's chunks past its own events decode to no events.
   int n_grp = 0;
-  for (int i = lane; i < a.spw; i += kWave) n_grp = max(n_grp, real_count(blockIdx.y * a.spw + i));
-  n_grp = __builtin_amdgcn_readfirstlane(wave_max(n_grp));
+  if (a.blist) {
+    n_grp = n_list;
+  } else {
+    for (int i = lane; i < a.spw; i += kWave)
+      n_grp = max(n_grp, real_count(blockIdx.y * a.spw + i));
+    n_grp = __builtin_amdgcn_readfirstlane(wave_max(n_grp));
+  }
   const int nchunks = (n_grp + kWave - 1) / kWave;
   const float* tb = a.times + (size_t)(live ? b : 0) * L;
   const int32_t* sb_src = a.src + (size_t)(live ? b : 0) * L;
@@ -762,14 +782,38 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int jl = n_eff - 1;
   float t_n = 0.0f;
   int s_n = -1;
-  if (dec && jl >= 0) { t_n = tb[min(lane, jl)]; s_n = sb_src[min(lane, jl)]; }
+  // With a list: the original indices of the next chunk's events (jo_n) and of the one
+  // after (jo_nn), the index loaded two chunks ahead and the event one chunk ahead.
+  int jo_n = 0, jo_nn = 0;
+  if (dec) {
+    if (a.blist) {
+      if (n_list > 0) {
+        jo_n = lst[min(lane, n_list - 1)];
+        jo_nn = lst[min(kWave + lane, n_list - 1)];
+        t_n = tb[jo_n];
+        s_n = sb_src[jo_n];
+      }
+    } else if (jl >= 0) {
+      t_n = tb[min(lane, jl)];
+      s_n = sb_src[min(lane, jl)];
+    }
+  }
   // Decoding wave: chunk k into record buffer k % 2 (and, merge mode, sub-band 0: the
   // chunk's event times and plane positions into event buffer k % 3).
   auto decode = [&](int k) {
     const int bf = k & 1;
-    const int j = k * kWave + lane;
+    int j = k * kWave + lane;
     const int tv = time_ms(t_n), sv = s_n;
-    if (jl >= 0) {
+    if (a.blist) {
+      // list position -> original index (past the list: not real)
+      j = j < n_list ? jo_n : n_eff;
+      if (n_list > 0) {
+        t_n = tb[jo_nn];
+        s_n = sb_src[jo_nn];
+        jo_n = jo_nn;
+        jo_nn = lst[min((k + 2) * kWave + lane, n_list - 1)];
+      }
+    } else if (jl >= 0) {
       const int j2 = min(j + kWave, jl);
       t_n = tb[j2];
       s_n = sb_src[j2];

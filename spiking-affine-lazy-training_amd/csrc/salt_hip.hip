@@ -175,6 +175,77 @@ __global__ void __launch_bounds__(64) compact_kernel(CompactArgs a, const int32_
     }
 }
 
+// ------------------------------------------------------------------ row-band event lists
+
+// Row-band plans: for every (stream, band of R output rows) the events whose candidate
+// rows [ceil((y+P-K+1)/S), floor((y+P)/S)] meet the band (the decode's row test; it
+// keeps a superset of the events with a candidate there), as original indices in order,
+// so that a band's work-group decodes its events alone instead of the whole stream.
+struct BandArgs {
+  int L, R, H, n_rb, K, S, P, HWin, Win, n_src, cap;
+  float rHWin, rWin, rS;
+  const int32_t* src;
+  const int32_t* n_real;
+  int32_t* cnt;   // [B][n_rb]
+  int32_t* off;   // [B][n_rb]: first entry of the band's list in the stream's region
+  int32_t* list;  // [B][cap]
+};
+
+// Whether source s (an input pixel) has candidate rows in [r0, r1).
+__device__ __forceinline__ bool band_meets(const BandArgs& a, int s, int r0, int r1) {
+  s = min(s, a.n_src - 1);
+  int ch, y, lo, hi;
+  if (a.n_src <= (1 << 22)) {
+    ch = div_small(s, a.HWin, a.rHWin);
+    y = div_small(s - ch * a.HWin, a.Win, a.rWin);
+    lo = div_small(y + a.P - a.K + a.S + a.K * a.S, a.S, a.rS) - a.K;
+    hi = div_small(y + a.P, a.S, a.rS);
+  } else {
+    ch = s / a.HWin;
+    y = (s - ch * a.HWin) / a.Win;
+    lo = floordiv_pos(y + a.P - a.K + a.S, a.S);
+    hi = (y + a.P) / a.S;
+  }
+  return max(lo, r0) <= min(hi, r1 - 1);
+}
+
+// One wave per (band, stream): blockIdx.x = band.  PASS 0 counts the band's events;
+// PASS 1 writes them at the band's offset (the stream's earlier bands' counts).  Four
+// windows of 64 events per iteration keep four loads in flight.
+template <int PASS>
+__global__ void __launch_bounds__(64) band_list_kernel(BandArgs a) {
+  const int lane = threadIdx.x;
+  const int rb = blockIdx.x, b = blockIdx.y;
+  const int nr = a.n_real[b];
+  const int n_eff = nr < 0 ? 0 : (nr < a.L ? nr : a.L);
+  const int r0 = rb * a.R, r1 = min(a.H, r0 + a.R);
+  const int32_t* src = a.src + (size_t)b * a.L;
+  int pos = 0;
+  if (PASS == 1) {
+    for (int t = lane; t < rb; t += kWave) pos += a.cnt[b * a.n_rb + t];
+    pos = __builtin_amdgcn_readlane(wave_incl_scan(pos), kWave - 1);
+    if (lane == 0) a.off[b * a.n_rb + rb] = pos;
+  }
+  int32_t* const out = a.list + (size_t)b * a.cap;
+  for (int base = 0; base < n_eff; base += 4 * kWave) {
+    int sv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = base + u * kWave + lane;
+      sv[u] = j < n_eff ? src[j] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = base + u * kWave + lane;
+      const bool in = sv[u] >= 0 && band_meets(a, sv[u], r0, r1);
+      const uint64_t m = __ballot(in);
+      if (PASS == 1 && in) out[pos + lanes_below(m)] = j;
+      pos += __popcll(m);
+    }
+  }
+  if (PASS == 0 && lane == 0) a.cnt[b * a.n_rb + rb] = pos;
+}
+
 // ------------------------------------------------------------------ hash
 
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {
@@ -609,8 +680,22 @@ size_t compact_bytes(size_t mask_bytes, int B, int L) {
 size_t mask_only_conv(const ConvPlan& pl, const salt_layer_desc* d, int B, int L) {
   return (size_t)B * L * d->oc * pl.WPO * 4;
 }
+// Row-band event lists (band_list_kernel): entries per stream, as an event's candidate
+// rows (NC of them) meet at most ceil((NC-1)/R) + 1 bands of R rows; 0 when lists are
+// off (SALT_CONV_BANDLIST=0, for comparisons) or would not fit 32-bit indices.
+long band_cap(const ConvPlan& pl, int L) {
+  const char* e = getenv("SALT_CONV_BANDLIST");
+  if (pl.merge || (e && e[0] == '0')) return 0;
+  const long cap = (long)L * ((pl.NC - 1 + pl.R - 1) / pl.R + 1);
+  return cap <= INT_MAX ? cap : 0;
+}
+size_t band_bytes(const ConvPlan& pl, int B, int L) {
+  const long cap = band_cap(pl, L);
+  return cap ? (size_t)B * pl.n_rb * 2 * 4 + (size_t)B * cap * 4 : 0;
+}
 size_t mask_bytes_conv(const ConvPlan& pl, const salt_layer_desc* d, int B, int L) {
-  return pl.merge ? 0 : compact_bytes(mask_only_conv(pl, d, B, L), B, L);
+  if (pl.merge) return 0;
+  return masks_end(compact_bytes(mask_only_conv(pl, d, B, L), B, L)) + band_bytes(pl, B, L);
 }
 size_t mask_only_fc(const FcPlan& pl, int B, int L) { return (size_t)B * L * pl.words * 4; }
 size_t mask_bytes_fc(const FcPlan& pl, int B, int L) {
@@ -700,6 +785,25 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     a.v_final = res->d_v_final; a.v_min = res->d_v_min; a.v_max = res->d_v_max;
     a.stats = res->d_stats;
     a.masks = static_cast<uint32_t*>(d_workspace);
+    a.blist = nullptr; a.bcnt = nullptr; a.boff = nullptr; a.bcap = 0;
+    if (const long cap = band_cap(pl, L)) {  // row bands: each band's events, listed
+      BandArgs ba;
+      ba.L = L; ba.R = pl.R; ba.H = pl.H; ba.n_rb = pl.n_rb; ba.K = desc->k; ba.S = desc->s;
+      ba.P = desc->p; ba.HWin = a.g.HWin; ba.Win = desc->w_in; ba.n_src = desc->ic * a.g.HWin;
+      ba.cap = (int)cap; ba.rHWin = a.g.rHWin; ba.rWin = a.g.rWin; ba.rS = a.g.rS;
+      ba.src = in->d_src; ba.n_real = in->d_n_real;
+      ba.cnt = reinterpret_cast<int32_t*>(
+          static_cast<char*>(d_workspace) +
+          masks_end(compact_bytes(mask_only_conv(pl, desc, B, L), B, L)));
+      ba.off = ba.cnt + (size_t)B * pl.n_rb;
+      ba.list = ba.off + (size_t)B * pl.n_rb;
+      const dim3 bgrid(pl.n_rb, B);
+      hipLaunchKernelGGL(band_list_kernel<0>, bgrid, dim3(kWave), 0, st, ba);
+      HIP_TRY(hipGetLastError());
+      hipLaunchKernelGGL(band_list_kernel<1>, bgrid, dim3(kWave), 0, st, ba);
+      HIP_TRY(hipGetLastError());
+      a.blist = ba.list; a.bcnt = ba.cnt; a.boff = ba.off; a.bcap = ba.cap;
+    }
     if (!pl.merge) {
       if ((rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
       if ((rc = fill(reinterpret_cast<int32_t*>(a.masks), 0,

@@ -43,7 +43,7 @@ def _qp(**kw):
     return _lib.QParams(**base)
 
 
-def test_workspace_size_is_host_only():
+def test_workspace_size_is_host_only(monkeypatch):
     size = ctypes.c_size_t(123)
     rc = _lib.lib().salt_layer_workspace_size(ctypes.byref(_desc_fc()), ctypes.byref(_qp()), 2,
                                              10, 0, ctypes.byref(size))
@@ -52,11 +52,17 @@ def test_workspace_size_is_host_only():
     d = _lib.LayerDesc()
     d.kind, d.ic, d.h_in, d.w_in, d.oc, d.k, d.s, d.p = _lib.SALT_LAYER_CONV, 2, 128, 128, 32, 3, 1, 0
     d.max_queue_len, d.max_out_spikes = 100, 16
+    # partitioned (row bands): per-event spike masks, then one spike count per (stream,
+    # 2048-event compaction segment), then (unless turned off) each band's event list
+    masks_and_counts = 64 * 1000 * 32 * 4 + 64 * 1 * 4
+    monkeypatch.setenv("SALT_CONV_BANDLIST", "0")
     rc = _lib.lib().salt_layer_workspace_size(ctypes.byref(d), ctypes.byref(_qp()), 64, 1000, 0,
                                              ctypes.byref(size))
-    # partitioned: per-event spike masks, then one spike count per (stream, 2048-event
-    # compaction segment)
-    assert rc == 0 and size.value == 64 * 1000 * 32 * 4 + 64 * 1 * 4
+    assert rc == 0 and size.value == masks_and_counts
+    monkeypatch.delenv("SALT_CONV_BANDLIST")
+    rc = _lib.lib().salt_layer_workspace_size(ctypes.byref(d), ctypes.byref(_qp()), 64, 1000, 0,
+                                             ctypes.byref(size))
+    assert rc == 0 and size.value > masks_and_counts + 64 * 1000 * 4
 
 
 @pytest.mark.parametrize("kw", [dict(f_a=16), dict(i_V=31), dict(q_bits=12), dict(n_table=0),

@@ -200,6 +200,32 @@ def test_conv_many_iterations_per_step_match_oracle(pair, monkeypatch):
         assert_layer_equal(out, ref, tag=f"iterations pair {pair} {case}")
 
 
+@pytest.mark.parametrize("lists", ["0", "1"])
+def test_conv_row_bands_with_and_without_event_lists(lists, monkeypatch):
+    """Row-band plans (planes above the LDS size) whose work-groups decode their band's
+    event list, or the whole stream (SALT_CONV_BANDLIST=0): same streams, registers and
+    extremes as the oracle, for stride 1 and for stride 2 with padding (events meeting
+    two bands), uniform and clustered sources."""
+    monkeypatch.setenv("SALT_CONV_BANDLIST", lists)
+    for mi, (case, clustered) in enumerate([((1, 130, 130, 4, 3, 1, 0, 3, 700), False),
+                                            ((2, 200, 200, 4, 5, 2, 2, 3, 600), True)]):
+        ic, h, w, oc, k, s, p, B, L = case
+        rng = np.random.default_rng(1300 + 10 * int(lists) + mi)
+        layer = ConvLayer(name="c", ic=ic, h_in=h, w_in=w, oc=oc, k=k, s=s, p=p, init_k=1.0,
+                          max_queue_len=int(rng.choice([L + 1, max(2, L // 25)])),
+                          max_out_spikes=4 * L * oc)
+        params, rm = _params(rng, layer.weight_shape, layer.n_neurons, oc, MODES[mi + 1], 8,
+                             ["channel", "neuron"][mi])
+        times, src, n_real = _events(rng, B, L, ic * h * w)
+        if clustered:
+            src = _clustered_sources(rng, B, L, ic, h, w, 3 * k)
+        print("band lists", lists, "case", case, flush=True)
+        out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+        geom, prm, cap = oracle_spec(layer, params, rm)
+        ref = O.layer_forward(geom, prm, times, src, n_real, cap)
+        assert_layer_equal(out, ref, tag=f"band lists {lists} {case}")
+
+
 def test_without_neuron_extremes_same_streams_and_registers():
     rng = np.random.default_rng(5)
     layer = ConvLayer(name="c", ic=2, h_in=34, w_in=34, oc=16, k=5, s=2, p=0, init_k=1.0,
