@@ -28,8 +28,8 @@ METRIC = "input events/sec (batch, 1 MI355X) bit-exact vs salt_core/quant; % HBM
 HBM_PEAK_GBS = 8000.0                     # MI355X HBM3E
 LDS_PEAK_GBS = 256 * 128 * 2.4            # 256 CUs x 128 B/clk x 2.4 GHz = 78.6 TB/s
 # Measured HBM traffic per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by a copy
-# of known size); see the file for the commands that produced it.
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_c3_nmnist_net.json")
+# of known size), one file per workload; each file names the commands that produced it.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_{workload}.json")
 COPY_BYTES = 1 << 30                      # --copy-calibration: bytes read (and written)
 
 
@@ -47,10 +47,11 @@ def copy_calibration() -> int:
     return 0
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of one layer kernel from the committed profile, or None."""
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of one layer kernel of one workload from the committed
+    profile, or None when that workload has no traffic profile."""
     try:
-        with open(TRAFFIC_FILE, encoding="utf-8") as f:
+        with open(TRAFFIC_FILE.format(workload=workload), encoding="utf-8") as f:
             return json.load(f)["per_launch_bytes"].get(kernel)
     except (OSError, KeyError, ValueError):
         return None
@@ -202,7 +203,7 @@ def main() -> int:
     lds_frac, hbm_frac = lds_gbs / LDS_PEAK_GBS, hbm_gbs / HBM_PEAK_GBS
     roofline = {"bound": "hbm", "kernel": dom["name"], "launch_ms": round(dom["ms"], 4),
                 "achieved": round(hbm_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(hbm_frac, 6), "traffic": measured_traffic(dom["name"]),
+                "frac": round(hbm_frac, 6), "traffic": measured_traffic(w.name, dom["name"]),
                 "algorithmic_bytes": dom["hbm_bytes"],
                 "lds": {"achieved": round(lds_gbs, 2), "peak": LDS_PEAK_GBS, "unit": "GB/s",
                         "frac": round(lds_frac, 5), "algorithmic_bytes": dom["lds_bytes"]},

@@ -7,7 +7,7 @@
 // event, the first against t = 0), so the codes of 64 events are looked up at once,
 // one per lane, and read back per event with v_readlane.  The event's weight column
 // comes from the transposed (n_in, n_out) copy -- from LDS when the slice's columns fit
-// (WLDS), else from global memory -- and is loaded one event ahead.
+// (WLDS), else from global memory -- and is loaded two events ahead.
 #pragma once
 
 #include <type_traits>
@@ -57,7 +57,7 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
   // WLDS: lane e holds the LDS index of its event's weight row, multiplied out once per
   // chunk, so that no scalar instruction waits for a v_readlane in the loop.
   const int rowv = WLDS ? sv * sw : 0;
-  // An event's operands, fetched one event ahead: its decay code and, per neuron, its
+  // An event's operands, fetched ahead of its step: its decay code and, per neuron, its
   // weight.  Lanes past the slice read a valid weight of the slice (col is clamped) and
   // are never reported; their threshold is unreachable.
   auto load = [&](QT (&q)[NPL], int& A, int e) {  // past the chunk: a harmless reload
@@ -106,21 +106,35 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
       }
     }
   };
-  // Two events per iteration with two operand sets, each loaded one event before its
-  // use: the loads' latency is covered by an event of arithmetic and no register has to
-  // be copied or widened before its use (either would wait for the load).
-  QT qa[NPL], qb[NPL];
-  int Aa = 0, Ab = 0;
-  load(qa, Aa, 0);
+  // Three events per iteration with three operand sets, each loaded two events before
+  // its use: the loads' latency is covered by two events of arithmetic and no register
+  // has to be copied or widened before its use (either would wait for the load).  The
+  // scheduling barriers keep each load where it is written: left alone, the compiler
+  // sinks a load past the preceding event's arithmetic to just before its own use, and
+  // the event then waits for the whole LDS latency.
+  QT q0[NPL], q1[NPL], q2[NPL];
+  int A0 = 0, A1 = 0, A2 = 0;
+  load(q0, A0, 0);
+  load(q1, A1, 1);
   int e = 0;
   auto run = [&](auto lo_only, auto fv0) {
-    for (; e + 1 < ne; e += 2) {
-      load(qb, Ab, e + 1);
-      step(e, qa, Aa, lo_only, fv0);
-      load(qa, Aa, e + 2);
-      step(e + 1, qb, Ab, lo_only, fv0);
+    // invariant at the loop head: q0/A0 hold event e, q1/A1 event e + 1
+    for (; e + 2 < ne; e += 3) {
+      load(q2, A2, e + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      step(e, q0, A0, lo_only, fv0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(q0, A0, e + 3);
+      __builtin_amdgcn_sched_barrier(0);
+      step(e + 1, q1, A1, lo_only, fv0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(q1, A1, e + 4);
+      __builtin_amdgcn_sched_barrier(0);
+      step(e + 2, q2, A2, lo_only, fv0);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (e < ne) step(e++, qa, Aa, lo_only, fv0);
+    if (e < ne) step(e++, q0, A0, lo_only, fv0);
+    if (e < ne) step(e++, q1, A1, lo_only, fv0);
   };
   const bool lo = DIRECT && NPL == 1 && sw <= 32;
   if (fV == 0) {
@@ -143,8 +157,8 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
     if (__builtin_expect(__ballot(cnt != 0) != 0, 0)) {  // readout layers rarely fire
       const int incl = wave_incl_scan(cnt);
       const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
-      int pos = out_base + incl - cnt;
       const float te = (float)tv;  // this lane's event time
+      int pos = out_base + incl - cnt;
 #pragma unroll
       for (int k = 0; k < NPL; ++k) {
         uint64_t bits = sp[k];
