@@ -20,15 +20,15 @@ using QType = int32_t;
 #endif
 
 template <int NPL, int F>
-hipError_t fc_entry(const FcArgs& a, dim3 grid, size_t lds, hipStream_t st) {
+hipError_t fc_entry(const FcArgs& a, dim3 grid, int waves, size_t lds, hipStream_t st) {
   constexpr bool kF24 = (F & kFcF24) != 0, kSat = (F & kFcSat) != 0, kWlds = (F & kFcWlds) != 0;
   static bool attr_set = false;
   auto fn = fc_layer_kernel<QType, NPL, kF24, kSat, kWlds>;
-  return launch_with_lds(reinterpret_cast<const void*>(fn), fn, &attr_set, grid, dim3(kWave),
-                         lds, st, a);
+  return launch_with_lds(reinterpret_cast<const void*>(fn), fn, &attr_set, grid,
+                         dim3(kWave * waves), lds, st, a);
 }
 
-using FcFn = hipError_t (*)(const FcArgs&, dim3, size_t, hipStream_t);
+using FcFn = hipError_t (*)(const FcArgs&, dim3, int, size_t, hipStream_t);
 
 template <int NPL, int... F>
 constexpr std::array<FcFn, sizeof...(F)> fc_table(std::integer_sequence<int, F...>) {
@@ -41,18 +41,18 @@ constexpr std::array<FcFn, sizeof...(F)> fc_table(std::integer_sequence<int, F..
 #define SALT_CAT(a, b) SALT_CAT2(a, b)
 
 hipError_t SALT_CAT(launch_fc_q, SALT_QBITS)(const FcArgs& a, int npl, int flags, dim3 grid,
-                                             size_t lds, hipStream_t st) {
+                                             int waves, size_t lds, hipStream_t st) {
   static constexpr auto t1 = fc_table<1>(std::make_integer_sequence<int, 8>{});
   static constexpr auto t2 = fc_table<2>(std::make_integer_sequence<int, 8>{});
   static constexpr auto t4 = fc_table<4>(std::make_integer_sequence<int, 8>{});
   static constexpr auto t8 = fc_table<8>(std::make_integer_sequence<int, 8>{});
   static constexpr auto t16 = fc_table<16>(std::make_integer_sequence<int, 8>{});
   switch (npl) {
-    case 1: return t1[flags & 7](a, grid, lds, st);
-    case 2: return t2[flags & 7](a, grid, lds, st);
-    case 4: return t4[flags & 7](a, grid, lds, st);
-    case 8: return t8[flags & 7](a, grid, lds, st);
-    default: return t16[flags & 7](a, grid, lds, st);
+    case 1: return t1[flags & 7](a, grid, waves, lds, st);
+    case 2: return t2[flags & 7](a, grid, waves, lds, st);
+    case 4: return t4[flags & 7](a, grid, waves, lds, st);
+    case 8: return t8[flags & 7](a, grid, waves, lds, st);
+    default: return t16[flags & 7](a, grid, waves, lds, st);
   }
 }
 

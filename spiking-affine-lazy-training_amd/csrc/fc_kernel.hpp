@@ -2,7 +2,11 @@
 // salt_core/connectivity/fc.py:20-61 and the scan of salt_core/quant/scan.py:22-132).
 //
 // One wave = one stream x one slice of 64*NPL neurons (neuron = n0 + k*64 + lane);
-// registers, extremes and thresholds stay in VGPRs.  Every real event updates every
+// registers, extremes and thresholds stay in VGPRs.  A stream's slices are either
+// separate work-groups that write spike masks (compacted afterwards), or the waves of one
+// work-group (up to kFcMaxWaves) that append to the stream directly: after each chunk the
+// waves exchange their per-event spike counts through LDS, so each places its own
+// spikes after those of the lower waves -- the (event, neuron) order of the reference.  Every real event updates every
 // neuron with the same decay code (the FC queue's dt is the gap to the previous real
 // event, the first against t = 0), so the codes of 64 events are looked up at once,
 // one per lane, and read back per event with v_readlane.  The event's weight column
@@ -15,6 +19,8 @@
 #include "salt_device.hpp"
 
 namespace salt {
+
+constexpr int kFcMaxWaves = 4;  // waves per stream of a directly appending FC layer
 
 struct FcArgs {
   int n_in, n_out, words;  // words: 32-bit spike-mask words per event (sliced layers)
@@ -46,14 +52,14 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
                                           int base, int ne, int tv, int sv, int Aj,
                                           int32_t (&V)[NPL], int32_t (&mn)[NPL],
                                           int32_t (&mx)[NPL], const int32_t (&vth)[NPL],
-                                          int& out_base) {
+                                          int& out_base, int32_t* merge) {
   const Quant& qz = a.qz;
   const int fa = qz.fa, fV = qz.fV;
   // The rounding constant in a VGPR for the whole loop: a VALU instruction reads one
   // scalar operand here, and the decay multiply-add's is the event's decay code.
   int rc = qz.rc;
   asm volatile("" : "+v"(rc));
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
   // WLDS: lane e holds the LDS index of its event's weight row, multiplied out once per
   // chunk, so that no scalar instruction waits for a v_readlane in the loop.
   const int rowv = WLDS ? sv * sw : 0;
@@ -154,11 +160,29 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
       sp[k] = ~(((uint64_t)khi[k] << 32) | klo[k]);
       cnt += __popcll(sp[k]);
     }
-    if (__builtin_expect(__ballot(cnt != 0) != 0, 0)) {  // readout layers rarely fire
-      const int incl = wave_incl_scan(cnt);
+    // Several waves per stream: the event's spikes in lower waves (lower neurons) come
+    // first.  The counts are double-buffered by chunk parity, so one barrier per chunk
+    // orders them: a wave rewrites a buffer only after every wave has passed the next
+    // chunk's barrier, i.e. has read it.
+    const int wpg = (int)(blockDim.x / kWave);
+    int lower = 0, evt = cnt;
+    if (wpg > 1) {
+      const int wave = (int)(threadIdx.x / kWave);
+      int32_t* mc = merge + ((base / kWave) & 1) * (kFcMaxWaves * kWave);
+      mc[wave * kWave + lane] = cnt;
+      __syncthreads();
+      evt = 0;
+      for (int w = 0; w < wpg; ++w) {
+        const int c = mc[w * kWave + lane];
+        evt += c;
+        lower += w < wave ? c : 0;
+      }
+    }
+    if (__builtin_expect(__ballot(evt != 0) != 0, 0)) {  // readout layers rarely fire
+      const int incl = wave_incl_scan(evt);
       const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
       const float te = (float)tv;  // this lane's event time
-      int pos = out_base + incl - cnt;
+      int pos = out_base + incl - evt + lower;
 #pragma unroll
       for (int k = 0; k < NPL; ++k) {
         uint64_t bits = sp[k];
@@ -178,17 +202,22 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
 }
 
 template <typename QT, int NPL, bool F24, bool SAT, bool WLDS>
-__global__ void __launch_bounds__(64) fc_layer_kernel(FcArgs a) {
+__global__ void __launch_bounds__(kFcMaxWaves * kWave) fc_layer_kernel(FcArgs a) {
   extern __shared__ int32_t dyn[];
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = (int)(threadIdx.x / kWave), wpg = (int)(blockDim.x / kWave);
   const int b = blockIdx.y;
-  const int n0 = blockIdx.x * (kWave * NPL);
+  const int n0 = (blockIdx.x * wpg + wave) * (kWave * NPL);
   const int sw = min(kWave * NPL, a.n_out - n0);  // neurons in this slice
   const Quant& qz = a.qz;
   int32_t* ext = dyn;
   QT* wl = reinterpret_cast<QT*>(dyn + (qz.n_table + 2));
+  // several waves per stream (never with WLDS): per-event spike counts, two chunk
+  // buffers of kFcMaxWaves x 64, then the waves' extremes
+  int32_t* merge = dyn + (qz.n_table + 2);
+  int32_t* red = merge + 2 * kFcMaxWaves * kWave;
   const QT* qt = static_cast<const QT*>(a.qt);
-  load_ext_table(ext, a.table, qz.n_table, qz.fa, lane, kWave);
+  load_ext_table(ext, a.table, qz.n_table, qz.fa, (int)threadIdx.x, (int)blockDim.x);
   if (WLDS)
     for (int i = lane; i < a.n_in * sw; i += kWave) {
       const int r = i / sw;
@@ -245,10 +274,10 @@ __global__ void __launch_bounds__(64) fc_layer_kernel(FcArgs a) {
     t_prev = rdlane(tv, ne - 1);
     if (a.direct)
       fc_events<QT, NPL, F24, SAT, WLDS, true>(a, wl, qt, col, sw, n0, b, base, ne, tv, sv, Aj,
-                                               V, mn, mx, vth, out_base);
+                                               V, mn, mx, vth, out_base, merge);
     else
       fc_events<QT, NPL, F24, SAT, WLDS, false>(a, wl, qt, col, sw, n0, b, base, ne, tv, sv,
-                                                Aj, V, mn, mx, vth, out_base);
+                                                Aj, V, mn, mx, vth, out_base, merge);
   }
   // Pad columns (j >= n_real) are identity with code 0 (connectivity/fc.py:32, :60-61):
   // their value before write-back is the final register.
@@ -269,9 +298,20 @@ __global__ void __launch_bounds__(64) fc_layer_kernel(FcArgs a) {
   }
   vmin_l = wave_min(vmin_l);
   vmax_l = wave_max(vmax_l);
+  if (a.direct && wpg > 1) {  // the stream's extremes over its waves
+    if (lane == 0) {
+      red[2 * wave] = vmin_l;
+      red[2 * wave + 1] = vmax_l;
+    }
+    __syncthreads();
+    for (int w = 0; w < wpg; ++w) {
+      vmin_l = min(vmin_l, red[2 * w]);
+      vmax_l = max(vmax_l, red[2 * w + 1]);
+    }
+  }
   const int ovf = (vmin_l < -qz.half || vmax_l > qz.half - 1) ? 1 : 0;
   if (a.direct) {
-    if (lane == 0) {
+    if (threadIdx.x == 0) {
       a.out_n[b] = out_base;
       a.stats[b * 4 + 0] = vmin_l;
       a.stats[b * 4 + 1] = vmax_l;
@@ -279,7 +319,7 @@ __global__ void __launch_bounds__(64) fc_layer_kernel(FcArgs a) {
       a.stats[b * 4 + 3] = ovf;
     }
     if (a.fill_pads)
-      for (int i = min(out_base, a.cap) + lane; i < a.cap; i += kWave) {
+      for (int i = min(out_base, a.cap) + (int)threadIdx.x; i < a.cap; i += (int)blockDim.x) {
         a.out_t[(size_t)b * a.cap + i] = kPadTime;
         a.out_s[(size_t)b * a.cap + i] = 0;
       }

@@ -30,8 +30,8 @@ SALT_CONV_NITS(SALT_DECLARE_CONV)
 enum : int { kFcF24 = 4, kFcSat = 2, kFcWlds = 1 };
 
 #define SALT_DECLARE_FC(B)                                                             \
-  hipError_t launch_fc_q##B(const FcArgs& a, int npl, int flags, dim3 grid, size_t lds, \
-                            hipStream_t st);
+  hipError_t launch_fc_q##B(const FcArgs& a, int npl, int flags, dim3 grid, int waves, \
+                            size_t lds, hipStream_t st);
 SALT_DECLARE_FC(8)
 SALT_DECLARE_FC(16)
 SALT_DECLARE_FC(32)

@@ -592,15 +592,41 @@ void choose_spw(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext
 }
 
 struct FcPlan {
-  int npl, n_slices, words, direct;
+  int npl, n_slices, words, direct, wpg;
 };
 
+// Waves per stream of a directly appending FC layer: SALT_FC_WAVES=n (1..kFcMaxWaves)
+// for tuning runs and tests, else 2.  Measured on MI355X: configuration 1 (128 neurons,
+// one stream) 0.42 -> 0.30 ms with two waves of 64 instead of one of 128; configuration 5
+// (1024 neurons, 4096 streams, ~180 spikes per event) 61.9 ms with one wave of 1024 or
+// two of 512, 70.3 ms with four of 256 -- its time is set by the L2 requests of the
+// spike stores (one cache line per lane), which more waves only contend for.
+int fc_waves_limit() {
+  const char* e = getenv("SALT_FC_WAVES");
+  const int n = e ? atoi(e) : 2;
+  return std::max(1, std::min(n, kFcMaxWaves));
+}
+
+// One stream's neurons go to wpg waves of 64*npl neurons (npl a power of two <= 16).
+// Up to kFcMaxWaves x 1024 neurons the waves form one work-group that appends to the
+// stream directly; beyond, each slice of 1024 is a work-group writing spike masks.
+// Several waves of fewer neurons each, rather than one wave of many: a wave of 1024
+// neurons needs over 256 registers (one wave per SIMD, nothing hides its memory
+// waits), and each wave's chain of events is shorter.
 int32_t plan_fc(const salt_layer_desc* d, FcPlan* pl) {
-  const int need = (d->n_out + kWave - 1) / kWave;
+  const int need = (d->n_out + kWave - 1) / kWave;  // 64-neuron words
+  const int wmax = fc_waves_limit();
   int npl = 1;
-  while (npl < need && npl < 16) npl *= 2;
+  if (need <= 16 * wmax) {
+    while (npl * wmax < need) npl *= 2;
+    pl->wpg = (need + npl - 1) / npl;               // no wave without a neuron
+    pl->n_slices = 1;
+  } else {
+    npl = 16;
+    pl->wpg = 1;
+    pl->n_slices = (need + npl - 1) / npl;
+  }
   pl->npl = npl;
-  pl->n_slices = (d->n_out + kWave * npl - 1) / (kWave * npl);
   pl->words = (d->n_out + 31) / 32;
   pl->direct = pl->n_slices == 1;
   return 0;
@@ -838,8 +864,10 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
   const size_t sw = (size_t)std::min(kWave * pl.npl, desc->n_out);
   const size_t wbytes = (size_t)desc->n_in * sw * (prm->q_bits / 8);
   const size_t tbytes = (size_t)(prm->n_table + 2) * 4;
-  const bool wlds = wbytes + tbytes <= kFcWeightLds;
-  const size_t lds = tbytes + (wlds ? wbytes : 0);
+  // the waves of a multi-wave work-group read weights from global memory (L2)
+  const bool wlds = pl.wpg == 1 && wbytes + tbytes <= kFcWeightLds;
+  const size_t merge = pl.wpg > 1 ? (size_t)(2 * kFcMaxWaves * kWave + 2 * kFcMaxWaves) * 4 : 0;
+  const size_t lds = tbytes + (wlds ? wbytes : 0) + merge;
   if (lds > (size_t)kLdsMax) return fail(-3, "decay table too long for LDS");
   if (!launch) return 0;
   FcArgs a;
@@ -855,9 +883,9 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
   const int flags = (f24 ? kFcF24 : 0) | (sat ? kFcSat : 0) | (wlds ? kFcWlds : 0);
   const dim3 grid(pl.n_slices, B);
   switch (prm->q_bits) {
-    case 8: HIP_TRY(launch_fc_q8(a, pl.npl, flags, grid, lds, st)); break;
-    case 16: HIP_TRY(launch_fc_q16(a, pl.npl, flags, grid, lds, st)); break;
-    default: HIP_TRY(launch_fc_q32(a, pl.npl, flags, grid, lds, st)); break;
+    case 8: HIP_TRY(launch_fc_q8(a, pl.npl, flags, grid, pl.wpg, lds, st)); break;
+    case 16: HIP_TRY(launch_fc_q16(a, pl.npl, flags, grid, pl.wpg, lds, st)); break;
+    default: HIP_TRY(launch_fc_q32(a, pl.npl, flags, grid, pl.wpg, lds, st)); break;
   }
   if (!pl.direct) {
     CompactArgs c;

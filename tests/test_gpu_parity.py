@@ -104,6 +104,29 @@ def test_fc_matches_oracle(case, mi):
     assert_layer_equal(out, ref, tag=str(case))
 
 
+
+@pytest.mark.parametrize("waves", ["1", "2", "4"])
+def test_fc_waves_per_stream_match_oracle(waves, monkeypatch):
+    """Dense firing (thresholds of a few units) with the neurons of a stream on 1, 2 or 4
+    waves (SALT_FC_WAVES): the waves' spikes merged per event in neuron order, a capacity
+    cut inside a chunk, and, with one wave, slices of 1024 neurons writing spike masks."""
+    monkeypatch.setenv("SALT_FC_WAVES", waves)
+    for mi, (n_in, n_out, B, L) in enumerate([(37, 10, 6, 300), (64, 130, 4, 200), (100, 300, 4, 150),
+                                              (50, 1024, 3, 130), (200, 1500, 2, 100)]):
+        rng = np.random.default_rng(4400 + 10 * mi + int(waves))
+        for cap in (L * n_out, 1 + L * n_out // 7):
+            layer = FCLayer(name="f", n_in=n_in, n_out=n_out, init_k=1.0, max_out_spikes=cap)
+            params, rm = _params(rng, layer.weight_shape, n_out, n_out, MODES[mi], [8, 16, 32][mi % 3],
+                                 "scalar")
+            params = params._replace(v_th_int=np.int32(rng.integers(1, 8)))
+            times, src, n_real = _events(rng, B, L, n_in)
+            print("fc waves", waves, (n_in, n_out, B, L), "cap", cap, flush=True)
+            out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+            geom, prm, ocap = oracle_spec(layer, params, rm)
+            ref = O.layer_forward(geom, prm, times, src, n_real, ocap)
+            assert int(ref["out_n"].sum()) > 64 * B, "the case must fire densely"
+            assert_layer_equal(out, ref, tag=f"waves {waves} {n_out} {cap}")
+
 @pytest.mark.parametrize("spw", [2, 3, 4, 5])
 def test_conv_streams_per_work_group_match_oracle(spw, monkeypatch):
     """Several streams per work-group (forced through SALT_CONV_SPW): streams of different
