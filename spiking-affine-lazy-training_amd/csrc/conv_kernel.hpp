@@ -92,6 +92,8 @@ struct ConvArgs {
   int32_t* v_max;
   int32_t* stats;
   uint32_t* masks;
+  int32_t* seg_cnt;  // masks only: spikes per (stream, kCompactSeg events), [B][nseg]
+  int nseg;
 };
 
 // Spare positions.  A lane without a candidate in an event reads and writes a spare
@@ -387,6 +389,7 @@ enum ConvMode { kStage = 0, kMask = 1 };
 struct ConvSink {
   int b;
   uint32_t* masks;
+  int32_t* seg_cnt;  // this stream's row of per-segment spike counts
   int L, OC, WPO, Gi;
 };
 
@@ -525,6 +528,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
         const size_t w = ((size_t)sk.b * sk.L + r1.y) * (size_t)(sk.OC * sk.WPO) +
                          (size_t)(c.oc_lane + it * sk.Gi) * sk.WPO + (c.cand >> 5);
         atomicOr(&sk.masks[w], 1u << (c.cand & 31));
+        atomicAdd(&sk.seg_cnt[r1.y / kCompactSeg], 1);  // the compaction skips empty segments
       }
     }
     r = rn;
@@ -743,6 +747,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   int vtc[NIT];
   ConvSink sk;
   sk.b = b; sk.masks = a.masks; sk.L = a.L; sk.OC = g.OC; sk.WPO = a.WPO; sk.Gi = Gi;
+  sk.seg_cnt = a.seg_cnt ? a.seg_cnt + (size_t)min(b, a.B - 1) * a.nseg : nullptr;
 
   const int L = a.L;
   auto real_count = [&](int bi) {

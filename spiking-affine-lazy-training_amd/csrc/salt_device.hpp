@@ -13,6 +13,9 @@
 namespace salt {
 
 constexpr int kWave = 64;
+// Events per compaction segment: spike masks become a stream segment by segment, so that
+// a stream's walk and its padding spread over many waves.
+constexpr int kCompactSeg = 2048;
 constexpr float kPadTime = 1e12f;  // salt_core/stream.py:13
 
 // Quantisation parameters of one layer, uniform over the launch.

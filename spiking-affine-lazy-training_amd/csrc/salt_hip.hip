@@ -78,11 +78,12 @@ struct CompactArgs {
 };
 
 // Spike bitmasks -> ordered stream, in segments of kCompactSeg events so that a stream's
-// walk and its padding spread over many waves: compact_count_kernel sums each segment's
-// spikes, compact_kernel (one wave per segment) starts its part of the stream after the
-// earlier segments' spikes.  Words are in neuron order and bits within a word too, so
-// walking them gives the (event, neuron) order of salt_core/stream.py:24-46.
-constexpr int kCompactSeg = 2048;
+// walk and its padding spread over many waves: the per-segment spike counts come from
+// the layer kernel (conv: one atomic per spike) or compact_count_kernel (FC slices);
+// compact_kernel (one wave per segment) starts its part of the stream after the earlier
+// segments' spikes and reads no mask of a segment without spikes.  Words are in neuron
+// order and bits within a word too, so walking them gives the (event, neuron) order of
+// salt_core/stream.py:24-46.
 
 int compact_segments(int L) { return std::max(1, (L + kCompactSeg - 1) / kCompactSeg); }
 
@@ -121,7 +122,7 @@ __global__ void __launch_bounds__(64) compact_kernel(CompactArgs a, const int32_
   before = __builtin_amdgcn_readlane(wave_incl_scan(before), kWave - 1);
   all = __builtin_amdgcn_readlane(wave_incl_scan(all), kWave - 1);
   int out_base = before;
-  const int j_end = min(n_eff, (s + 1) * kCompactSeg);
+  const int j_end = seg_cnt[b * nseg + s] > 0 ? min(n_eff, (s + 1) * kCompactSeg) : 0;
   for (int base = s * kCompactSeg; base < j_end; base += kWave) {
     const int j = base + lane;
     const bool ok = j < j_end;
@@ -729,13 +730,20 @@ size_t mask_bytes_fc(const FcPlan& pl, int B, int L) {
 }
 
 // Launches the two compaction kernels over a layer's spike masks.
+// counted: the layer kernel has already summed each segment's spikes.
+int32_t* compact_seg_counts(void* ws, size_t mask_bytes) {
+  return reinterpret_cast<int32_t*>(static_cast<char*>(ws) + masks_end(mask_bytes));
+}
+
 int32_t launch_compact(const CompactArgs& c, int B, int L, size_t mask_bytes, void* ws,
-                       hipStream_t st) {
+                       hipStream_t st, bool counted = false) {
   const int nseg = compact_segments(L);
-  int32_t* const seg = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + masks_end(mask_bytes));
+  int32_t* const seg = compact_seg_counts(ws, mask_bytes);
   const dim3 grid(nseg, B);
-  hipLaunchKernelGGL(compact_count_kernel, grid, dim3(kWave), 0, st, c, seg, nseg);
-  HIP_TRY(hipGetLastError());
+  if (!counted) {
+    hipLaunchKernelGGL(compact_count_kernel, grid, dim3(kWave), 0, st, c, seg, nseg);
+    HIP_TRY(hipGetLastError());
+  }
   hipLaunchKernelGGL(compact_kernel, grid, dim3(kWave), 0, st, c, (const int32_t*)seg, nseg);
   HIP_TRY(hipGetLastError());
   return 0;
@@ -799,6 +807,7 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     if (!launch) return 0;
     choose_spw(desc, prm, B, ext, &pl);
     ConvArgs a;
+    a.seg_cnt = nullptr; a.nseg = 0;  // set for mask plans below
     a.g = conv_geom(desc, pl);
     a.WPO = pl.WPO;
     a.G = pl.G; a.Gi = pl.Gi; a.ncg = pl.ncg; a.nsb = pl.nsb; a.Rw = pl.Rw; a.R = pl.R;
@@ -835,6 +844,9 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
       if ((rc = fill(reinterpret_cast<int32_t*>(a.masks), 0,
                      mask_only_conv(pl, desc, B, L) / 4, st)))
         return rc;
+      a.nseg = compact_segments(L);
+      a.seg_cnt = compact_seg_counts(d_workspace, mask_only_conv(pl, desc, B, L));
+      if ((rc = fill(a.seg_cnt, 0, (size_t)B * a.nseg, st))) return rc;
     }
     const int flags = (sat ? kConvSat : 0) | (ext ? kConvExt : 0) |
                       (prm->v_th_kind == SALT_VTH_PER_NEURON ? kConvVthN : 0) |
@@ -850,7 +862,8 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
       c.n_real = in->d_n_real; c.masks = a.masks; c.cap = out->cap;
       c.fill_pads = out->fill_pads; c.out_t = out->d_times; c.out_s = out->d_src;
       c.out_n = out->d_n;
-      if ((rc = launch_compact(c, B, L, mask_only_conv(pl, desc, B, L), d_workspace, st)))
+      if ((rc = launch_compact(c, B, L, mask_only_conv(pl, desc, B, L), d_workspace, st,
+                               /*counted=*/true)))
         return rc;
     }
     return 0;
