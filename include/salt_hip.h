@@ -38,7 +38,7 @@ extern "C" {
 #define SALT_LAYER_FC 0
 #define SALT_LAYER_CONV 1
 
-#define SALT_VTH_NONE 0        /* v_th_int = None: never fires (quant/params.py:244-245) */
+#define SALT_VTH_NONE 0        /* v_th_int = None: never fires (quant/params.py:14-15)   */
 #define SALT_VTH_SCALAR 1      /* one threshold for every neuron                         */
 #define SALT_VTH_PER_CHANNEL 2 /* conv: one per output channel; FC: one per neuron       */
 #define SALT_VTH_PER_NEURON 3  /* one per neuron, neuron = oc*H*W + y*W + x              */
@@ -49,7 +49,7 @@ extern "C" {
 #define SALT_SATURATE 1
 
 /* Layer geometry and capacities.  Mirrors ConvLayer (salt_core/layers/conv.py:30-53) and
- * FCLayer (salt_core/layers/fc.py:246-256); the float-training fields are not needed. */
+ * FCLayer (salt_core/layers/fc.py:23-38); the float-training fields are not needed. */
 typedef struct {
     int32_t kind;            /* SALT_LAYER_FC or SALT_LAYER_CONV                       */
     int32_t n_in, n_out;     /* FC                                                     */
@@ -115,7 +115,8 @@ int32_t salt_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes, void* stre
 int32_t salt_stream_sync(void* stream);
 
 /* Transpose FC weight codes from the reference layout (n_out, n_in)
- * (salt_core/layers/fc.py:274-276) to the (n_in, n_out) layout the FC kernels read;
+ * (FCLayer.weight_shape, salt_core/layers/fc.py:58-60) to the (n_in, n_out) layout the
+ * FC kernels read;
  * replaces the per-event gather q[:, src] of salt_core/connectivity/fc.py:54-61. */
 int32_t salt_fc_transpose(const void* d_q_ref, void* d_q_t, int32_t n_out, int32_t n_in,
                           int32_t q_bits, void* stream);

@@ -67,6 +67,10 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_layer_forward.argtypes = [ctypes.POINTER(_Geom), ctypes.POINTER(_QParams),
                                               i32, i32, p, p, p, i32, p, p, p, p, p, p, p, i32]
         _lib.oracle_layer_forward.restype = ctypes.c_int
+        _lib.oracle_layer_forward_hashed.argtypes = [ctypes.POINTER(_Geom),
+                                                     ctypes.POINTER(_QParams), i32, i32, p, p,
+                                                     p, i32, p, p, p, p, p, p, i32]
+        _lib.oracle_layer_forward_hashed.restype = ctypes.c_int
         _lib.oracle_stream_hash.argtypes = [p, p, i32, i32]
         _lib.oracle_stream_hash.restype = ctypes.c_uint64
     return _lib
@@ -131,9 +135,11 @@ def n_neurons(geom: dict) -> int:
 
 
 def layer_forward(geom: dict, params: dict, times, src, n_real, cap: int,
-                  nthreads: int = 0, want_stream: bool = True) -> dict:
+                  nthreads: int = 0, want_stream: bool = True, hashed: bool = False) -> dict:
     """One layer over a batch.  times/src: (B, L); n_real: (B,).  Returns numpy arrays:
-    out_times/out_src (B, cap), out_n (B,), v_final/v_min/v_max (B, N), needed_queue (B,)."""
+    out_times/out_src (B, cap), out_n (B,), v_final/v_min/v_max (B, N), needed_queue (B,).
+    hashed: instead of out_times/out_src, out_hash (B,) uint64 -- each stream's
+    stream_hash() -- without allocating the (B, cap) output."""
     times = np.ascontiguousarray(times, dtype=np.float32)
     src = np.ascontiguousarray(src, dtype=np.int32)
     n_real = np.ascontiguousarray(n_real, dtype=np.int32).reshape(-1)
@@ -165,6 +171,15 @@ def layer_forward(geom: dict, params: dict, times, src, n_real, cap: int,
     out = {"out_n": np.zeros(B, np.int32), "v_final": np.zeros((B, N), np.int32),
            "v_min": np.zeros((B, N), np.int32), "v_max": np.zeros((B, N), np.int32),
            "needed_queue": np.zeros(B, np.int32)}
+    if hashed:
+        out["out_hash"] = np.zeros(B, np.uint64)
+        rc = lib().oracle_layer_forward_hashed(
+            ctypes.byref(g), ctypes.byref(qp), B, L, _ptr(times), _ptr(src), _ptr(n_real), cap,
+            _ptr(out["out_n"]), _ptr(out["out_hash"]), _ptr(out["v_final"]), _ptr(out["v_min"]),
+            _ptr(out["v_max"]), _ptr(out["needed_queue"]), nthreads)
+        if rc != 0:
+            raise ValueError("oracle_layer_forward_hashed rejected its arguments")
+        return out
     if want_stream:
         out["out_times"] = np.zeros((B, cap), np.float32)
         out["out_src"] = np.zeros((B, cap), np.int32)

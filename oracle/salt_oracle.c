@@ -141,6 +141,21 @@ static void sb_push(spike_buf* b, int32_t j, int32_t neuron) {
     b->n++;
 }
 
+static inline uint64_t mix64(uint64_t z);
+
+/* One kept entry of the output stream: written where asked, and mixed into the
+ * order-sensitive hash of oracle_stream_hash (entry index i, time bits, source). */
+static inline void put_entry(int64_t i, float t, int32_t s, float* out_times, int32_t* out_src,
+                             uint64_t* hash_acc) {
+    if (out_times) out_times[i] = t;
+    if (out_src) out_src[i] = s;
+    if (hash_acc) {
+        uint32_t tb;
+        memcpy(&tb, &t, 4);
+        *hash_acc += mix64(mix64((uint64_t)i) ^ (((uint64_t)tb << 32) | (uint32_t)s));
+    }
+}
+
 /*
  * salt_core/stream.py:24-64.  The reference takes the first `cap` spikes of
  * nonzero(spike_mask) -- neuron-major, then queue column -- and sorts them stably by
@@ -150,17 +165,18 @@ static void sb_push(spike_buf* b, int32_t j, int32_t neuron) {
  */
 static void emit_stream(const spike_buf* sb, int32_t n_neurons, int32_t cap,
                         const float* times, int32_t L, float* out_times, int32_t* out_src,
-                        int32_t* out_n, int32_t* scratch_counts) {
+                        int32_t* out_n, int32_t* scratch_counts, uint64_t* out_hash) {
     int64_t total = sb->n;
     *out_n = (int32_t)total;
-    if (!out_times && !out_src) return;
+    uint64_t acc = 0;
+    uint64_t* hacc = out_hash ? &acc : NULL;
+    if (!out_times && !out_src && !out_hash) return;
     int64_t written = 0;
     if (total <= cap) {
         for (int64_t i = 0; i < total; i++) {
             int32_t j = sb->j[i];
             int32_t jj = j < L ? j : L - 1; /* stream.py:37-38 clamps the pad index */
-            if (out_times) out_times[written] = times[jj];
-            if (out_src) out_src[written] = sb->neuron[i];
+            put_entry(written, times[jj], sb->neuron[i], out_times, out_src, hacc);
             written++;
         }
     } else {
@@ -179,8 +195,7 @@ static void emit_stream(const spike_buf* sb, int32_t n_neurons, int32_t cap,
             if (rank < cap) {
                 int32_t j = sb->j[i];
                 int32_t jj = j < L ? j : L - 1;
-                if (out_times) out_times[written] = times[jj];
-                if (out_src) out_src[written] = n;
+                put_entry(written, times[jj], n, out_times, out_src, hacc);
                 written++;
             }
         }
@@ -189,6 +204,7 @@ static void emit_stream(const spike_buf* sb, int32_t n_neurons, int32_t cap,
         if (out_times) out_times[i] = PAD_TIME;
         if (out_src) out_src[i] = 0; /* nonzero(..., fill_value=0), stream.py:60 */
     }
+    if (out_hash) *out_hash = mix64(acc + (uint64_t)(uint32_t)total * 0x2545F4914F6CDD1DULL);
 }
 
 /* ---------------------------------------------------------------- layer */
@@ -335,12 +351,12 @@ static void conv_stream(const oracle_geom* g, const oracle_qparams* p, const ste
     }
 }
 
-int oracle_layer_forward(const oracle_geom* g, const oracle_qparams* prm, int32_t B,
-                         int32_t L, const float* times, const int32_t* src,
-                         const int32_t* n_real, int32_t cap, float* out_times,
-                         int32_t* out_src, int32_t* out_n, int32_t* v_final,
-                         int32_t* v_min, int32_t* v_max, int32_t* needed_queue,
-                         int32_t nthreads) {
+static int layer_forward_impl(const oracle_geom* g, const oracle_qparams* prm, int32_t B,
+                              int32_t L, const float* times, const int32_t* src,
+                              const int32_t* n_real, int32_t cap, float* out_times,
+                              int32_t* out_src, int32_t* out_n, uint64_t* out_hash,
+                              int32_t* v_final, int32_t* v_min, int32_t* v_max,
+                              int32_t* needed_queue, int32_t nthreads) {
     if (!g || !prm || B < 0 || L < 0 || cap < 0 || !out_n) return -1;
     if (prm->n_table < 1 || prm->f_a < 0 || prm->f_a > 15 || prm->f_V < 0 ||
         prm->i_V + prm->f_V < 1 || prm->i_V + prm->f_V > 30)
@@ -396,7 +412,8 @@ int oracle_layer_forward(const oracle_geom* g, const oracle_qparams* prm, int32_
              * spikes (key L) after them in neuron order: the buffer is already in
              * the stable key order of stream.py:40. */
             emit_stream(&sb, N, cap, tb, L, out_times ? out_times + (int64_t)b * cap : NULL,
-                        out_src ? out_src + (int64_t)b * cap : NULL, &out_n[b], counts);
+                        out_src ? out_src + (int64_t)b * cap : NULL, &out_n[b], counts,
+                        out_hash ? &out_hash[b] : NULL);
             if (v_final) memcpy(v_final + (int64_t)b * N, V, sizeof(int32_t) * (size_t)N);
             if (v_min) memcpy(v_min + (int64_t)b * N, vmn, sizeof(int32_t) * (size_t)N);
             if (v_max) memcpy(v_max + (int64_t)b * N, vmx, sizeof(int32_t) * (size_t)N);
@@ -411,6 +428,26 @@ int oracle_layer_forward(const oracle_geom* g, const oracle_qparams* prm, int32_
         free(act);
     }
     return 0;
+}
+
+int oracle_layer_forward(const oracle_geom* g, const oracle_qparams* prm, int32_t B,
+                         int32_t L, const float* times, const int32_t* src,
+                         const int32_t* n_real, int32_t cap, float* out_times,
+                         int32_t* out_src, int32_t* out_n, int32_t* v_final,
+                         int32_t* v_min, int32_t* v_max, int32_t* needed_queue,
+                         int32_t nthreads) {
+    return layer_forward_impl(g, prm, B, L, times, src, n_real, cap, out_times, out_src, out_n,
+                              NULL, v_final, v_min, v_max, needed_queue, nthreads);
+}
+
+int oracle_layer_forward_hashed(const oracle_geom* g, const oracle_qparams* prm, int32_t B,
+                                int32_t L, const float* times, const int32_t* src,
+                                const int32_t* n_real, int32_t cap, int32_t* out_n,
+                                uint64_t* out_hash, int32_t* v_final, int32_t* v_min,
+                                int32_t* v_max, int32_t* needed_queue, int32_t nthreads) {
+    if (!out_hash) return -1;
+    return layer_forward_impl(g, prm, B, L, times, src, n_real, cap, NULL, NULL, out_n,
+                              out_hash, v_final, v_min, v_max, needed_queue, nthreads);
 }
 
 /* ---------------------------------------------------------------- stream hash */

@@ -39,7 +39,7 @@ typedef struct {
 
 typedef struct {
     const int32_t* q;      /* weight codes as int32, reference layout: FC (n_out, n_in),
-                              conv (oc, ic, k, k) -- quant/params.py:241-242             */
+                              conv (oc, ic, k, k) -- quant/params.py:11-12             */
     const int32_t* table;  /* decay_table_int, length n_table (dt = 1 .. n_table)         */
     int32_t n_table;
     const int32_t* v_th;   /* see v_th_kind                                              */
@@ -80,6 +80,15 @@ int oracle_layer_forward(const oracle_geom* g, const oracle_qparams* prm, int32_
                          int32_t* out_src, int32_t* out_n, int32_t* v_final,
                          int32_t* v_min, int32_t* v_max, int32_t* needed_queue,
                          int32_t nthreads);
+
+/* oracle_layer_forward without the output stream: per stream, its spike count and the
+ * hash oracle_stream_hash would give of the stream it writes (no B*cap buffers, for
+ * streams of millions of spikes).  v_final/v_min/v_max/needed_queue as above. */
+int oracle_layer_forward_hashed(const oracle_geom* g, const oracle_qparams* prm, int32_t B,
+                                int32_t L, const float* times, const int32_t* src,
+                                const int32_t* n_real, int32_t cap, int32_t* out_n,
+                                uint64_t* out_hash, int32_t* v_final, int32_t* v_min,
+                                int32_t* v_max, int32_t* needed_queue, int32_t nthreads);
 
 /* Order-sensitive 64-bit hash of one output stream, for streams too large to copy
  * back.  Each entry i < min(n, cap) contributes mix64(mix64(i) ^ (time_bits << 32 | src));

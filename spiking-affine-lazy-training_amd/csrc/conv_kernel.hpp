@@ -851,7 +851,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     const int incl = wave_incl_scan(tot);
     const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
     const int2 ev = evt0[(k % kConvEvtBufs) * kWave + lane];  // read with every lane active
-    const float te = (float)ev.x;
+    const float te = ms_time(ev.x);
     int pos = out_base + (incl - tot) + before;
     const uint64_t* const stg_cg = reinterpret_cast<const uint64_t*>(
         swave0 + cg * lay.wave_words + lay.stg) + bf * kWave * NIT + lane * NIT;

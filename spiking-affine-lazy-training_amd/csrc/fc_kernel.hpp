@@ -181,7 +181,7 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
     if (__builtin_expect(__ballot(evt != 0) != 0, 0)) {  // readout layers rarely fire
       const int incl = wave_incl_scan(evt);
       const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
-      const float te = (float)tv;  // this lane's event time
+      const float te = ms_time(tv);  // this lane's event time
       int pos = out_base + incl - evt + lower;
 #pragma unroll
       for (int k = 0; k < NPL; ++k) {

@@ -69,13 +69,19 @@ __device__ __forceinline__ void load_ext_table(int32_t* ext, const int32_t* tabl
     ext[i] = i == 0 ? (1 << fa) : (i <= n_table ? table[i - 1] : 0);
 }
 
-// Times are float32 holding integer ms below 2^31 (checked on the host), so the
-// conversion is exact; the integer difference equals the reference's float32
-// difference wherever it selects a table entry (see the kernels' notes).
-__device__ __forceinline__ int time_ms(float t) { return (int)t; }
+// Times are float32 holding integer ms in [0, 2^31) (checked on the host); the unsigned
+// conversion is exact up to 2^32, so even a time rounded up to 2^31 by the float32 cast
+// keeps its value.  Differences are taken in 32-bit wrap-around arithmetic and read as
+// unsigned: for non-decreasing times that is the exact gap, which equals the reference's
+// float32 difference wherever the gap selects a table entry (gaps up to 2^21 are exact
+// in float32 differences of such times).  Spike times go back to float through
+// ms_time().
+__device__ __forceinline__ int time_ms(float t) { return (int)(uint32_t)t; }
+__device__ __forceinline__ float ms_time(int t) { return (float)(uint32_t)t; }
 
+// Extended-table index of a gap: 0 (identity), 1..n (table), n + 1 (decay to 0).
 __device__ __forceinline__ int decay_slot(int dt, int n_table) {
-  return min(max(dt, 0), n_table + 1);
+  return (int)min((uint32_t)dt, (uint32_t)n_table + 1u);
 }
 
 __device__ __forceinline__ int floordiv_pos(int a, int s) {  // s > 0

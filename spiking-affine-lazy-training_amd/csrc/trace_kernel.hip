@@ -29,10 +29,11 @@ namespace {
 
 constexpr int kTraceBlock = 256;
 
+// Decay code of a gap (times non-decreasing; the wrap-around difference read unsigned).
 __device__ __forceinline__ int32_t trace_decay(const TraceArgs& a, int dt) {
-  const int n = a.qz.n_table;
-  if (dt <= 0) return 1 << a.qz.fa;  // identity column
-  return dt <= n ? a.table[dt - 1] : 0;
+  const uint32_t d = (uint32_t)dt, n = (uint32_t)a.qz.n_table;
+  if (d == 0) return 1 << a.qz.fa;  // identity column
+  return d <= n ? a.table[d - 1] : 0;
 }
 
 __device__ __forceinline__ int32_t trace_vth(const TraceArgs& a, int neuron, int channel) {

@@ -11,7 +11,7 @@ from salt_amd.layers.base import LayerOutput, check_leading_axis
 
 @dataclass(frozen=True)
 class FCLayer:
-    """salt_core/layers/fc.py:238-352."""
+    """salt_core/layers/fc.py:23-135."""
     name: str
     n_in: int
     n_out: int
@@ -74,7 +74,7 @@ class FCLayer:
 
 @dataclass(frozen=True)
 class FCSpec:
-    """FCLayer without n_in, completed by Network.build (salt_core/layers/fc.py:355-369)."""
+    """FCLayer without n_in, completed by Network.build (salt_core/layers/fc.py:139-154)."""
     n_out: int
     name: str | None = None
     options: Mapping[str, Any] = field(default_factory=dict)
@@ -85,5 +85,5 @@ class FCSpec:
 
 
 def fc(n_out: int, *, name: str | None = None, **options: Any) -> FCSpec:
-    """salt_core/layers/fc.py:372-374."""
+    """salt_core/layers/fc.py:157-158."""
     return FCSpec(n_out=n_out, name=name, options=options)

@@ -40,7 +40,10 @@ class InputEvents(NamedTuple):
         real_times = times[is_real]
         if not np.all(real_times == np.floor(real_times)):
             raise ValueError("事件時間必須是整數毫秒 (event times must be integer ms)")
-        if np.any(real_times < 0) or np.any(real_times >= _MAX_EVENT_TIME):
+        # The range is also checked on the float32 values the kernels receive: float64
+        # times in [2^31 - 64, 2^31) round up to 2^31 there.
+        if (np.any(real_times < 0) or np.any(real_times >= _MAX_EVENT_TIME)
+                or np.any(real_times.astype(np.float32) >= np.float32(_MAX_EVENT_TIME))):
             raise ValueError(f"事件時間必須在 [0, 2^31) 裡,拿到的範圍是 "
                              f"[{real_times.min()}, {real_times.max()}]")
         both_real = is_real[..., 1:]

@@ -47,7 +47,7 @@ def test_layer_literals_on_gpu(golden, section):
 
 
 def test_readout_multiplies_back_per_neuron_scale():
-    """salt_core/tests/test_quant_backend.py:426-442: registers [100, 90], f_V=1,
+    """salt_core/tests/test_quant_backend.py:257-273: registers [100, 90], f_V=1,
     s_c=[1, 2] -> [50, 90]; argmax flips after readout."""
     layer = FCLayer(name="out", n_in=1, n_out=2, init_k=5.0, tau=4.0, max_out_spikes=4)
     params = QuantizedLayerParams(q=np.array([[50], [45]]), decay_table_int=build_decay_table_int(4, 4.0),
@@ -61,7 +61,7 @@ def test_readout_multiplies_back_per_neuron_scale():
 
 
 def test_network_chains_conv_into_fc_like_manual_chaining():
-    """salt_core/tests/test_quant_backend.py:329-352: run_network equals calling the layers
+    """salt_core/tests/test_quant_backend.py:160-183: run_network equals calling the layers
     one by one and feeding each output stream to the next."""
     conv = ConvLayer(name="conv", ic=1, h_in=3, w_in=3, oc=1, k=3, s=1, p=0, init_k=5.0, tau=4.0,
                      max_queue_len=10, max_out_spikes=9)

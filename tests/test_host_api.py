@@ -30,6 +30,15 @@ def test_checked_rejects_invalid_real_times(times, message):
         InputEvents.checked(np.array(times, dtype=np.float64), np.zeros(3, np.int32), np.array(3))
 
 
+def test_checked_rejects_times_that_round_to_2_31_in_float32():
+    """A float64 time just below 2^31 passes the reference's check but is 2^31 once cast to
+    the float32 the kernels read; it is rejected here with the range message.  The largest
+    float32 below 2^31 (2^31 - 128) is accepted."""
+    with pytest.raises(ValueError, match=r"\[0, 2\^31\)"):
+        InputEvents.checked(np.array([1.0, 2.0 ** 31 - 10]), np.zeros(2, np.int32), np.array(2))
+    InputEvents.checked(np.array([1.0, 2.0 ** 31 - 128]), np.zeros(2, np.int32), np.array(2))
+
+
 def test_checked_accepts_batch():
     """salt_core/tests/test_network.py:39-42."""
     InputEvents.checked(np.array([[1.0, 2.0, 3.0], [4.0, 5.0, 0.0]]), np.zeros((2, 3), np.int32),
