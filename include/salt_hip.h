@@ -184,6 +184,23 @@ int32_t salt_layer_trace(const salt_layer_desc* desc, const salt_qparams* prm,
                          const salt_events_in* in, int32_t steps, int32_t* d_v_steps,
                          float* d_event_ms, uint8_t* d_flags, void* stream);
 
+/*
+ * salt_layer_forward without a workspace argument and without any device allocation.
+ * It has no counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * The workspace is a static per-device scratch array of SALT_STATIC_SCRATCH_BYTES, held
+ * from the library's load until the process ends; a layer and batch that need more
+ * (salt_layer_workspace_size) are rejected with -1 and a message.  Every call on one
+ * device shares that device's array, which keeps the last call's contents (the call
+ * clears what must start at zero): calls that overlap on one device race, so issue them
+ * on one stream, or synchronise between streams.  Inputs, outputs and results are the
+ * caller's, as for salt_layer_forward.
+ */
+#define SALT_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+int32_t salt_layer_forward_static(const salt_layer_desc* desc, const salt_qparams* prm,
+                                  const salt_events_in* in, const salt_events_out* out,
+                                  const salt_layer_result* result, void* stream);
+
 /* Order-sensitive 64-bit hash per stream, for streams too large to copy back.
  * With mix64 = the splitmix64 finaliser (add 0x9E3779B97F4A7C15, then xor-shift-multiply
  * by 0xBF58476D1CE4E5B9 and 0x94D049BB133111EB), entry i < min(n, cap) contributes

@@ -1139,3 +1139,56 @@ int32_t salt_network_forward(int32_t n_layers, const salt_layer_desc* descs,
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------------ static scratch
+
+namespace {
+
+// Workspace of salt_layer_forward_static: one array per device, held until the process
+// ends.  In host code `scratch` names a host-side stand-in, not device memory, so its
+// device address is looked up once per device (with that device current) and only that
+// address is ever passed to kernels or fills.
+constexpr size_t kScratchBytes = SALT_STATIC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+int32_t scratch_address(void** out) {
+  static std::mutex mu;
+  static std::map<int, void*> per_device;
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> g(mu);
+  auto it = per_device.find(dev);
+  if (it == per_device.end()) {
+    void* ptr = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) return fail(-2, "hipGetSymbolAddress(scratch) gave a null address");
+    it = per_device.emplace(dev, ptr).first;
+  }
+  *out = it->second;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t salt_layer_forward_static(const salt_layer_desc* desc, const salt_qparams* prm,
+                                  const salt_events_in* in, const salt_events_out* out,
+                                  const salt_layer_result* res, void* stream) {
+  if (!in) return fail(-1, "null events descriptor");
+  size_t need = 0;
+  int32_t rc = salt_layer_workspace_size(desc, prm, in->B, in->L,
+                                         res && res->d_v_min != nullptr, &need);
+  if (rc) return rc;
+  if (need > kScratchBytes)
+    return fail(-1,
+                "salt_layer_forward_static: this layer and batch need %zu bytes of scratch, "
+                "above the static maximum of %zu; use salt_layer_forward with a workspace",
+                need, kScratchBytes);
+  void* ptr = nullptr;
+  if ((rc = scratch_address(&ptr))) return rc;
+  if ((rc = layer_forward(desc, prm, in, out, res, ptr, kScratchBytes, nullptr, 0))) return rc;
+  return layer_forward(desc, prm, in, out, res, ptr, kScratchBytes, (hipStream_t)stream, 1);
+}
+
+}  // extern "C"

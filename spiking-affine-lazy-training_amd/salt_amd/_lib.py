@@ -20,6 +20,7 @@ SALT_LAYER_FC, SALT_LAYER_CONV = 0, 1
 SALT_VTH_NONE, SALT_VTH_SCALAR, SALT_VTH_PER_CHANNEL, SALT_VTH_PER_NEURON = 0, 1, 2, 3
 SALT_ROUND, SALT_TRUNCATE = 0, 1
 SALT_WRAP, SALT_SATURATE = 0, 1
+SALT_STATIC_SCRATCH_BYTES = 64 << 20  # salt_layer_forward_static's per-device scratch
 
 _i32 = ctypes.c_int32
 _p = ctypes.c_void_p
@@ -63,6 +64,9 @@ SIGNATURES = {
     "salt_layer_forward": ([ctypes.POINTER(LayerDesc), ctypes.POINTER(QParams),
                             ctypes.POINTER(EventsIn), ctypes.POINTER(EventsOut),
                             ctypes.POINTER(LayerResult), _p, ctypes.c_size_t, _p], _i32),
+    "salt_layer_forward_static": ([ctypes.POINTER(LayerDesc), ctypes.POINTER(QParams),
+                                   ctypes.POINTER(EventsIn), ctypes.POINTER(EventsOut),
+                                   ctypes.POINTER(LayerResult), _p], _i32),
     "salt_stream_hash": ([_p, _p, _p, _i32, _i32, _p, _p], _i32),
     "salt_layer_trace": ([ctypes.POINTER(LayerDesc), ctypes.POINTER(QParams),
                           ctypes.POINTER(EventsIn), _i32, _p, _p, _p, _p], _i32),
