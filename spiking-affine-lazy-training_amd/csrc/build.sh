@@ -28,3 +28,9 @@ if [ "$status" -ne 0 ]; then echo "build failed" >&2; exit 1; fi
 "$hipcc" --offload-arch=gfx950 -shared -fPIC -o "$out.tmp" "$obj"/*.o
 mv "$out.tmp" "$out"
 echo "built $out"
+# The LDS bandwidth probe bench.py's roofline uses: a library of its own, not linked into
+# the forward path.
+probe="$here/../salt_amd/libsalt_probe.so"
+"$hipcc" "${flags[@]}" -shared -o "$probe.tmp" "$here/lds_probe.hip"
+mv "$probe.tmp" "$probe"
+echo "built $probe"

@@ -134,3 +134,13 @@ def test_network_checks_every_layer_before_launching():
     rc = _lib.lib().salt_network_forward(2, d, q, ctypes.byref(ev_in), outs, res, 8, 1 << 40,
                                          None)
     assert rc == -1 and b"MAX_SHIFT_BITS" in _lib.lib().salt_last_error()
+
+
+def test_probe_library_exports_its_header():
+    """libsalt_probe.so (bench.py's LDS probe) exports what include/salt_probe.h declares."""
+    text = open(os.path.join(ROOT, "include", "salt_probe.h"), encoding="utf-8").read()
+    names = re.findall(r"^\s*int32_t\s+(salt_\w+)\s*\(", text, re.M)
+    assert names == ["salt_probe_lds"]
+    probe = ctypes.CDLL(os.path.join(os.path.dirname(_lib.LIB_PATH), "libsalt_probe.so"))
+    for name in names:
+        assert hasattr(probe, name), name
