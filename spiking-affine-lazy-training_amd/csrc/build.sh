@@ -19,6 +19,9 @@ pids=()
 for n in 1 2 3 4 8; do
   "$hipcc" "${flags[@]}" -DSALT_NIT=$n -c "$here/conv_inst.hip" -o "$obj/conv_$n.o" & pids+=($!)
 done
+for n in 1 2 3 4 5 6 7 8; do
+  "$hipcc" "${flags[@]}" -DSALT_PACK_IMAX=$n -c "$here/conv_packed_inst.hip" -o "$obj/pack_$n.o" & pids+=($!)
+done
 for q in 8 16 32; do
   "$hipcc" "${flags[@]}" -DSALT_QBITS=$q -c "$here/fc_inst.hip" -o "$obj/fc_$q.o" & pids+=($!)
 done

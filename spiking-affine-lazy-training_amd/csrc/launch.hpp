@@ -4,6 +4,7 @@
 #pragma once
 
 #include "conv_kernel.hpp"
+#include "conv_packed.hpp"
 #include "fc_kernel.hpp"
 
 namespace salt {
@@ -25,6 +26,19 @@ constexpr int kConvFlagCombos = 64;
                                 size_t lds, hipStream_t st);
 SALT_CONV_NITS(SALT_DECLARE_CONV)
 #undef SALT_DECLARE_CONV
+
+// Packed conv flags: bit 3 = no queue truncation possible, bit 2 = threshold array (per
+// channel or per neuron), bit 1 = per-neuron extremes, bit 0 = saturate.
+enum : int { kPackNoTrunc = 8, kPackVtha = 4, kPackExt = 2, kPackSat = 1 };
+constexpr int kPackFlagCombos = 16;
+
+// Iteration bounds with an instantiated packed kernel family.
+#define SALT_PACK_IMAXES(X) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
+#define SALT_DECLARE_PACK(N)                                                           \
+  hipError_t launch_pack_imax##N(const PackArgs& a, int flags, dim3 grid, dim3 block,  \
+                                 size_t lds, hipStream_t st);
+SALT_PACK_IMAXES(SALT_DECLARE_PACK)
+#undef SALT_DECLARE_PACK
 
 // FC flags: bit 2 = 24-bit high multiply, bit 1 = saturate, bit 0 = weights in LDS.
 enum : int { kFcF24 = 4, kFcSat = 2, kFcWlds = 1 };

@@ -592,6 +592,79 @@ void choose_spw(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext
   }
 }
 
+// ------------------------------------------------------------------ packed conv plan
+
+struct PackPlan {
+  int H, W, NC, ncg, Gw, spw, P, imax, Wp, VS, QS;
+  bool vtha;
+  size_t lds;
+};
+
+// The packed conv kernel runs only when asked for: SALT_CONV_PACKED=1, or
+// SALT_CONV_PACK="ncg,spw" (which also forces its channel groups and streams per
+// work-group).  Measured on MI355X it is slower than the channel-slot kernel on every
+// configuration (configuration 3 at B=1024: conv1 1.04 ms against 0.75, conv2 0.67
+// against 0.65; configuration 2: 0.95 against 0.69), so the channel-slot kernel is the
+// default.  Results never depend on the choice.
+bool packed_disabled() {
+  const char* e = getenv("SALT_CONV_PACKED");
+  if (e) return e[0] != '1';
+  return getenv("SALT_CONV_PACK") == nullptr;
+}
+bool pack_override(int* ncg, int* spw) {
+  const char* e = getenv("SALT_CONV_PACK");
+  return e && sscanf(e, "%d,%d", ncg, spw) == 2 && *ncg >= 1 && *spw >= 1;
+}
+
+size_t pack_lds_bytes(const salt_qparams* p, const PackPlan& pl, bool ext, bool notrunc) {
+  const PackLds l = pack_lds_layout(p->n_table, pl.NC * pl.NC, pl.ncg, pl.spw, pl.P, pl.VS, pl.QS,
+                                    pl.H * pl.Wp, pl.imax, ext, pl.vtha, notrunc);
+  return (size_t)l.words * 4;
+}
+
+// Plans the packed kernel for a conv layer whose output plane (all channels, with the
+// zero planes) fits in LDS with candidate grids of at most kPackMaxNC^2 positions.
+// Channel groups (waves per stream): enough for one wave per SIMD over the batch (a
+// stream's single wave when the batch fills the chip), each group at most 8 iterations
+// per event; streams per work-group: up to 4 independent single-wave streams sharing
+// the tables and codes.  Returns false when the layer does not qualify.
+bool plan_packed(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext, bool notrunc,
+                 PackPlan* pl) {
+  if (packed_disabled()) return false;
+  pl->H = (d->h_in + 2 * d->p - d->k) / d->s + 1;
+  pl->W = (d->w_in + 2 * d->p - d->k) / d->s + 1;
+  if (pl->H < 1 || pl->W < 1) return false;
+  pl->NC = (d->k - 1) / d->s + 1;
+  if (pl->NC > kPackMaxNC) return false;
+  pl->vtha = p->v_th_kind == SALT_VTH_PER_CHANNEL || p->v_th_kind == SALT_VTH_PER_NEURON;
+  const int OC = d->oc, cus = device_cus();
+  const int max_g = std::min(kPackMaxBlockWaves, OC);
+  int ncg = std::max(1, std::min(max_g, (4 * cus + std::max(B, 1) - 1) / std::max(B, 1)));
+  int spw = 0;
+  const bool forced = pack_override(&ncg, &spw);
+  ncg = std::min(ncg, max_g);
+  for (;; ++ncg) {
+    if (ncg > max_g) return false;
+    pl->ncg = ncg;
+    pl->Gw = (OC + ncg - 1) / ncg;
+    int imax = 0;
+    pl->P = pack_slots(pl->NC, pl->Gw, &imax);
+    if (imax <= 8) { pl->imax = imax; break; }
+  }
+  pl->Wp = pl->W;
+  pl->VS = pl->H * pl->W;
+  pl->QS = d->ic * d->k * d->k;
+  // streams per work-group: up to 4 (with one wave each) or 2 (with several), within the
+  // work-group size
+  const int spw_cap = kPackMaxBlockWaves / pl->ncg;
+  const int spw_max = std::min(spw_cap, forced ? spw : (pl->ncg == 1 ? 4 : 2));
+  for (pl->spw = std::max(1, std::min(spw_max, std::max(B, 1))); pl->spw >= 1; --pl->spw) {
+    pl->lds = pack_lds_bytes(p, *pl, ext, notrunc);
+    if (pl->lds <= (size_t)kLdsMax) return true;
+  }
+  return false;
+}
+
 struct FcPlan {
   int npl, n_slices, words, direct, wpg;
 };
@@ -769,6 +842,47 @@ hipError_t launch_conv(const ConvArgs& a, const ConvPlan& pl, int flags, int B,
   }
 }
 
+hipError_t launch_pack(const PackArgs& a, const PackPlan& pl, int flags, dim3 grid,
+                       hipStream_t st) {
+  const dim3 block(kWave * pl.ncg * pl.spw);
+  switch (pl.imax) {
+#define SALT_CASE(N) \
+    case N: return launch_pack_imax##N(a, flags, grid, block, pl.lds, st);
+    SALT_PACK_IMAXES(SALT_CASE)
+#undef SALT_CASE
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Enqueues one conv layer on the packed kernel (arguments already checked).
+int32_t launch_packed(const salt_layer_desc* desc, const salt_qparams* prm,
+                      const salt_events_in* in, const salt_events_out* out,
+                      const salt_layer_result* res, const Quant& qz, const PackPlan& pl, int B,
+                      int L, bool ext, bool sat, bool notrunc, hipStream_t st) {
+  PackArgs a;
+  a.g.IC = desc->ic; a.g.Win = desc->w_in; a.g.HWin = desc->h_in * desc->w_in; a.g.OC = desc->oc;
+  a.g.K = desc->k; a.g.S = desc->s; a.g.P = desc->p; a.g.H = pl.H; a.g.W = pl.W;
+  a.g.HW = pl.H * pl.W; a.g.NC = pl.NC; a.g.NC2 = pl.NC * pl.NC; a.g.mql = desc->max_queue_len;
+  a.g.Wp = pl.Wp;
+  a.g.rHWin = 1.0f / (float)a.g.HWin;  // correctly rounded on the host
+  a.g.rWin = 1.0f / (float)a.g.Win;
+  a.g.rS = 1.0f / (float)a.g.S;
+  a.ncls = pl.NC * pl.NC;
+  a.ncg = pl.ncg; a.Gw = pl.Gw; a.spw = pl.spw; a.B = B;
+  a.P = pl.P; a.VS = pl.VS; a.QS = pl.QS;
+  a.qz = qz; a.table = prm->d_decay_table; a.q = prm->d_q; a.q_bits = prm->q_bits;
+  a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
+  a.cap = out->cap; a.fill_pads = out->fill_pads;
+  a.out_t = out->d_times; a.out_s = out->d_src; a.out_n = out->d_n;
+  a.v_final = res->d_v_final; a.v_min = res->d_v_min; a.v_max = res->d_v_max;
+  a.stats = res->d_stats;
+  const int flags = (sat ? kPackSat : 0) | (ext ? kPackExt : 0) | (pl.vtha ? kPackVtha : 0) |
+                    (notrunc ? kPackNoTrunc : 0);
+  const dim3 grid((B + pl.spw - 1) / pl.spw);
+  HIP_TRY(launch_pack(a, pl, flags, grid, st));
+  return 0;
+}
+
 constexpr size_t kFcWeightLds = 40 * 1024;  // stage FC weight slices up to this size
 
 // Checks the arguments of one layer call (launch = 0) or, once they are known to be
@@ -798,8 +912,14 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
   const bool sat = prm->overflow_mode == SALT_SATURATE;
 
   if (desc->kind == SALT_LAYER_CONV) {
+    const bool notrunc = desc->max_queue_len >= L;
+    PackPlan pk;
+    if (plan_packed(desc, prm, B, ext, notrunc, &pk)) {
+      if (!launch) return 0;
+      return launch_packed(desc, prm, in, out, res, qz, pk, B, L, ext, sat, notrunc, st);
+    }
     ConvPlan pl;
-    rc = plan_conv(desc, prm, B, ext, desc->max_queue_len >= L, &pl);
+    rc = plan_conv(desc, prm, B, ext, notrunc, &pl);
     if (rc) return rc;
     const size_t need = mask_bytes_conv(pl, desc, B, L);
     if (workspace_bytes < need || (need && !d_workspace))
@@ -980,6 +1100,11 @@ int32_t salt_layer_workspace_size(const salt_layer_desc* desc, const salt_qparam
   if (rc) return rc;
   if (!bytes || B < 0 || L < 0) return fail(-1, "invalid batch shape");
   if (desc->kind == SALT_LAYER_CONV) {
+    PackPlan pk;
+    if (plan_packed(desc, prm, B, want_neuron_extremes != 0, desc->max_queue_len >= L, &pk)) {
+      *bytes = 0;  // the packed kernel keeps everything in LDS
+      return 0;
+    }
     ConvPlan pl;
     rc = plan_conv(desc, prm, B, want_neuron_extremes != 0, desc->max_queue_len >= L, &pl);
     if (rc) return rc;

@@ -129,9 +129,10 @@ def test_fc_waves_per_stream_match_oracle(waves, monkeypatch):
 
 @pytest.mark.parametrize("spw", [2, 3, 4, 5])
 def test_conv_streams_per_work_group_match_oracle(spw, monkeypatch):
-    """Several streams per work-group (forced through SALT_CONV_SPW): streams of different
+    """Channel-slot kernel, several streams per work-group (forced through SALT_CONV_SPW): streams of different
     lengths, an empty one, and a last work-group with slots past the batch (B = 7, 11)
     give the oracle's streams, registers and extremes."""
+    monkeypatch.setenv("SALT_CONV_PACKED", "0")  # the channel-slot kernel
     monkeypatch.setenv("SALT_CONV_SPW", str(spw))
     for mi, case in enumerate([(2, 34, 34, 16, 5, 2, 0, 7, 400), (16, 15, 15, 32, 3, 2, 0, 11, 400),
                                (2, 10, 10, 2, 3, 1, 0, 11, 200)]):
@@ -173,6 +174,7 @@ def test_conv_one_and_two_events_per_step_match_oracle(pair, monkeypatch):
     """Steps of one event and of two (forced through SALT_CONV_PAIR): uniform and
     clustered sources, whole-plane, sub-band and row-band plans, truncated and untruncated
     queues give the oracle's streams, registers and extremes."""
+    monkeypatch.setenv("SALT_CONV_PACKED", "0")  # the channel-slot kernel
     monkeypatch.setenv("SALT_CONV_PAIR", pair)
     cases = [((2, 34, 34, 16, 5, 2, 0, 6, 500), None, False), ((2, 34, 34, 16, 5, 2, 0, 6, 500), None, True),
              ((16, 15, 15, 32, 3, 2, 0, 6, 400), None, True), ((2, 12, 12, 8, 3, 1, 1, 5, 300), "2,2", True),
@@ -204,6 +206,7 @@ def test_conv_many_iterations_per_step_match_oracle(pair, monkeypatch):
     """One channel group per stream (SALT_CONV_PLAN=1,1) puts every channel in one wave:
     3 iterations per event for conv1's geometry (8 with two-event steps) and 2 for
     conv2's (4 with two-event steps), clustered sources."""
+    monkeypatch.setenv("SALT_CONV_PACKED", "0")  # the channel-slot kernel
     monkeypatch.setenv("SALT_CONV_PAIR", pair)
     monkeypatch.setenv("SALT_CONV_PLAN", "1,1")
     for mi, case in enumerate([(2, 34, 34, 16, 5, 2, 0, 5, 400), (16, 15, 15, 32, 3, 2, 0, 5, 400)]):
@@ -280,6 +283,7 @@ def test_repeat_runs_are_bitwise_identical():
 def test_conv_work_group_shapes_match_oracle(plan, monkeypatch):
     """Every work-group shape the planner can choose (channel groups x row sub-bands,
     forced through SALT_CONV_PLAN) gives the oracle's streams, registers and extremes."""
+    monkeypatch.setenv("SALT_CONV_PACKED", "0")  # the channel-slot kernel
     monkeypatch.setenv("SALT_CONV_PLAN", plan)
     for mi, case in enumerate([(2, 34, 34, 16, 5, 2, 0, 8, 400), (16, 15, 15, 32, 3, 2, 0, 8, 400),
                                (2, 12, 12, 8, 3, 1, 1, 8, 300)]):
@@ -296,3 +300,42 @@ def test_conv_work_group_shapes_match_oracle(plan, monkeypatch):
         geom, prm, cap = oracle_spec(layer, params, rm)
         ref = O.layer_forward(geom, prm, times, src, n_real, cap)
         assert_layer_equal(out, ref, tag=f"{plan} {case}")
+
+
+PACK_CASES = [
+    # (ic, h, w, oc, k, s, p, B, L)
+    (2, 34, 34, 16, 5, 2, 0, 7, 500),      # conv1 of the N-MNIST network: classes up to 3x3
+    (16, 15, 15, 32, 3, 2, 0, 7, 400),     # conv2: classes up to 2x2, 32 channels
+    (2, 20, 20, 6, 5, 1, 2, 5, 300),       # stride 1, padding: classes up to 5x5
+    (3, 9, 11, 5, 4, 3, 2, 7, 200),        # stride 3 > k / 2, odd plane
+    (1, 7, 7, 3, 1, 2, 0, 6, 120),         # k < s: pixels that reach no neuron
+    (2, 12, 12, 40, 3, 1, 1, 5, 200),      # many channels: several iterations at 3x3
+]
+
+
+@pytest.mark.parametrize("shape", ["1,1", "1,3", "1,4", "2,1", "2,2", "2,3", "3,1", "4,2", "8,1"])
+def test_conv_packed_shapes_match_oracle(shape, monkeypatch):
+    """The packed conv kernel (valid candidates packed per class of candidate rectangle)
+    with its channel groups x streams per work-group forced through SALT_CONV_PACK:
+    uniform and clustered sources, truncated and untruncated queues, every threshold kind,
+    both overflow modes, a short and an empty stream, and a last work-group with slots past
+    the batch give the oracle's streams, registers and extremes."""
+    monkeypatch.setenv("SALT_CONV_PACK", shape)
+    for mi, case in enumerate(PACK_CASES):
+        ic, h, w, oc, k, s, p, B, L = case
+        rng = np.random.default_rng(2100 + 17 * mi + int(shape[0]) * 3 + int(shape[-1]))
+        layer = ConvLayer(name="c", ic=ic, h_in=h, w_in=w, oc=oc, k=k, s=s, p=p, init_k=1.0,
+                          max_queue_len=int(rng.choice([L + 1, max(2, L // 25)])),
+                          max_out_spikes=int(rng.choice([4 * L * oc, 11])))
+        params, rm = _params(rng, layer.weight_shape, layer.n_neurons, oc, MODES[mi % 5],
+                             [8, 16, 32][mi % 3], ["scalar", "channel", "neuron", "none"][mi % 4])
+        times, src, n_real = _events(rng, B, L, ic * h * w)
+        n_real[2] = L // 9
+        if mi % 2:
+            src = _clustered_sources(rng, B, L, ic, h, w, 2 * k)
+        print("packed", shape, "case", case, "mql", layer.max_queue_len, "cap", layer.max_out_spikes,
+              flush=True)
+        out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+        geom, prm, cap = oracle_spec(layer, params, rm)
+        ref = O.layer_forward(geom, prm, times, src, n_real, cap)
+        assert_layer_equal(out, ref, tag=f"packed {shape} {case}")
