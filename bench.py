@@ -116,13 +116,18 @@ def lds_peak(out_path: str | None) -> int:
     return 0
 
 
+LAYER_KERNELS = ("layer_kernel", "packed_kernel")   # one dispatch per layer
+POST_KERNELS = ("compact_kernel",)                  # after their layer's kernel
+
+
 def digest_counters(src_dir: str, config: int, kind: str, out_path: str, command: str) -> int:
     """rocprofv3 counter CSVs (every *counter_collection.csv under src_dir) of a bench.py run
-    profiled with --kernel-include-regex layer_kernel -> per-layer means per dispatch.  The
-    layer kernels run in network order, so dispatch i (in dispatch-id order) is layer
-    i mod n_layers.  kind "sq": SQ_* instruction counts as they are; kind "traffic": the
-    HBM bytes FETCH_SIZE x f + WRITE_SIZE x w with f, w read from the copy calibration
-    files (copy_*.csv: the same counters for a COPY_BYTES device copy)."""
+    -> per-layer means per launch.  Layer kernels run in network order, so the i-th layer
+    kernel dispatch (in dispatch-id order) is layer i mod n_layers; other profiled kernels
+    (row-band list builds, fills, compactions) count towards the layer whose kernel follows
+    them, compactions towards the one they follow.  kind "sq": SQ_* counters as they are;
+    kind "traffic": the HBM bytes FETCH_SIZE x f + WRITE_SIZE x w with f, w read from the
+    copy calibration files (copy_*.csv: the same counters for a COPY_BYTES device copy)."""
     from salt_amd import workloads as W
     names = [l.name for l in W.CONFIGS[config]().network.layers]
     rows = {}
@@ -131,22 +136,52 @@ def digest_counters(src_dir: str, config: int, kind: str, out_path: str, command
         with open(path, newline="", encoding="utf-8") as f:
             for r in csv.DictReader(f):
                 key = ("copy" if is_copy else "run", path, int(r["Dispatch_Id"]))
-                rows.setdefault(key, {"kernel": r["Kernel_Name"]})[r["Counter_Name"]] = float(r["Counter_Value"])
+                v = rows.setdefault(key, {"kernel": r["Kernel_Name"]})
+                v[r["Counter_Name"]] = v.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
     runs, copies = {}, {}
     for (what, path, did), v in sorted(rows.items()):
         (copies if what == "copy" else runs).setdefault(path, []).append(v)
-    per_layer: dict[str, dict[str, list]] = {n: {} for n in names}
-    kernels = {}
+    per_launch: dict[str, list] = {n: [] for n in names}   # summed counters per layer launch
+    per_kernel: dict[str, dict[str, list]] = {}
+    kernels: dict[str, list] = {n: [] for n in names}
     for path, disp in runs.items():
-        for i, v in enumerate(disp):
-            name = names[i % len(names)]
-            kernels[name] = v["kernel"][:120]
+        i_layer, pending, last = 0, [], None
+        for v in disp:
+            k = v["kernel"]
+            short = k[:120]
             for c, x in v.items():
                 if c != "kernel":
-                    per_layer[name].setdefault(c, []).append(x)
-    means = {n: {c: sum(x) / len(x) for c, x in d.items()} for n, d in per_layer.items()}
-    out = {"what": f"per-dispatch means of rocprofv3 counters, layer kernels of {W.CONFIGS[config]().name}",
-           "command": command, "kernels": kernels, "per_layer": means}
+                    per_kernel.setdefault(short, {}).setdefault(c, []).append(x)
+            if any(t in k for t in LAYER_KERNELS):
+                name = names[i_layer % len(names)]
+                i_layer += 1
+                launch = {}
+                for u in pending + [v]:
+                    for c, x in u.items():
+                        if c != "kernel":
+                            launch[c] = launch.get(c, 0.0) + x
+                per_launch[name].append(launch)
+                for u in pending + [v]:
+                    if u["kernel"][:120] not in kernels[name]:
+                        kernels[name].append(u["kernel"][:120])
+                pending, last = [], name
+            elif any(t in k for t in POST_KERNELS) and last is not None and per_launch[last]:
+                for c, x in v.items():
+                    if c != "kernel":
+                        per_launch[last][-1][c] = per_launch[last][-1].get(c, 0.0) + x
+                if short not in kernels[last]:
+                    kernels[last].append(short)
+            else:
+                pending.append(v)
+    # each counter's mean over the launches that carry it (one pass per counter or group)
+    means = {}
+    for n, L in per_launch.items():
+        cs = sorted({c for d in L for c in d})
+        means[n] = {c: sum(d[c] for d in L if c in d) / sum(1 for d in L if c in d) for c in cs}
+    kmeans = {k: {c: sum(x) / len(x) for c, x in d.items()} for k, d in per_kernel.items()}
+    out = {"what": f"per-launch means of rocprofv3 counters, layers of {W.CONFIGS[config]().name} "
+                   "(each layer's kernels summed), and per-dispatch means per kernel",
+           "command": command, "kernels": kernels, "per_layer": means, "per_kernel": kmeans}
     if kind == "traffic":
         cal = {}
         for disp in copies.values():
@@ -158,10 +193,12 @@ def digest_counters(src_dir: str, config: int, kind: str, out_path: str, command
                         cal.setdefault(c, []).append(v[c])
         fac = {c: COPY_BYTES / (max(x) * 1024.0) for c, x in cal.items() if x}
         out["copy_calibration"] = {"bytes": COPY_BYTES, "factor": fac}
-        out["per_launch_bytes"] = {
-            n: round(m.get("FETCH_SIZE", 0) * 1024 * fac.get("FETCH_SIZE", 1.0)
-                     + m.get("WRITE_SIZE", 0) * 1024 * fac.get("WRITE_SIZE", 1.0))
-            for n, m in means.items()}
+
+        def hbm(m):
+            return round(m.get("FETCH_SIZE", 0) * 1024 * fac.get("FETCH_SIZE", 1.0)
+                         + m.get("WRITE_SIZE", 0) * 1024 * fac.get("WRITE_SIZE", 1.0))
+        out["per_launch_bytes"] = {n: hbm(m) for n, m in means.items()}
+        out["per_kernel_bytes"] = {k: hbm(m) for k, m in kmeans.items()}
     with open(out_path, "w", encoding="utf-8") as f:
         json.dump(out, f, indent=1)
         f.write("\n")

@@ -34,8 +34,12 @@
 // the chunk's barrier every wave places its own spikes in the stream's output, in the
 // order (event, channel group, iteration, lane) = (event, ascending neuron id) of
 // salt_core/stream.py:24-46, from a scan of all the stream's waves' counts.  With
-// several work-groups per stream (state above the LDS size) each wave sets per-event
-// spike bits in global memory instead, and a compaction kernel orders them.
+// several work-groups per stream (state above the LDS size: bands of rows) the waves
+// stage the same ballots; after the chunk's barrier, for each event with a spike in the
+// band, every wave stores its ballots as 64-bit spike words in global memory, in the
+// event's slot for this band, and marks the slot valid; a compaction kernel orders them.
+// Nothing is stored for an event without a spike in the band, and only the validity
+// words need clearing before the launch.
 //
 // One barrier per 64-event chunk, none inside the event loop: a wave's LDS operations
 // complete in program order, so event e+1 reads what event e wrote.  The decoding wave
@@ -58,7 +62,6 @@ struct ConvGeom {
 
 struct ConvArgs {
   ConvGeom g;
-  int WPO;  // spike-mask words per (event, channel)
   // partition: G channels per channel group in NIT iterations of Gi slots; ncg channel
   // groups x nsb sub-bands of Rw rows per work-group; R rows per work-group
   int G, Gi, ncg, nsb, Rw, R;
@@ -91,8 +94,14 @@ struct ConvArgs {
   int32_t* v_min;
   int32_t* v_max;
   int32_t* stats;
-  uint32_t* masks;
-  int32_t* seg_cnt;  // masks only: spikes per (stream, kCompactSeg events), [B][nseg]
+  // Row-band plans: an event reaches at most nslots consecutive bands, band x filling slot
+  // x % nslots of the event.  words: [B][L][nslots][ncg][NIT] spike words (lane l of
+  // channel group g's iteration it = slot l / NC2, candidate l % NC2), stored only for
+  // events with a spike in the band; valid: [B][L] bit per slot stored.
+  uint64_t* words;
+  uint32_t* valid;
+  int nslots;
+  int32_t* seg_cnt;  // row bands: spikes per (stream, kCompactSeg events), [B][nseg]
   int nseg;
 };
 
@@ -183,8 +192,8 @@ __host__ __device__ inline ConvLds conv_lds_layout(int n_table, int spw, int ncg
 struct ConvLane {
   int4* rec;
   int2* rec1;
-  uint64_t* stg;         // this chunk's spike ballots (kStage)
-  int32_t* wcnt;         // this chunk's spikes per event (kStage)
+  uint64_t* stg;         // this chunk's spike ballots
+  int32_t* wcnt;         // this chunk's spikes per event
   int2* tc;
   const int32_t* ext;
   const int32_t* qs;     // weight codes q*2^f_V
@@ -280,7 +289,7 @@ __device__ __forceinline__ void lds_st_tc(int addr, int t, int cnt) {
 // Decodes the events of one chunk (connectivity/conv.py:15-43), one per lane (time tv,
 // source sv, index j; real when j < n_eff and sv >= 0), against the rows [r0, r0+rn):
 // records {time, position base * 4, code base * 4, candidate mask low} + {mask high,
-// event index} for the events with a candidate there, compacted in order, followed by
+// idx} for the events with a candidate there, compacted in order, followed by
 // records with no candidate (mask 0) for the other lanes; with the two permanent ones
 // at indices kWave and kWave + 1, the two records after a chunk's last event cover
 // nothing, so the event loop reads two records ahead without a bounds test.  Returns
@@ -289,11 +298,12 @@ __device__ __forceinline__ void lds_st_tc(int addr, int t, int cnt) {
 // cnt (queue counts of a wave that keeps them, else null): each event adds one to the
 // count of every candidate position it has.
 // PAIR: the records go to steps of two events instead, and the number of steps is
-// returned (see below).
+// returned (see below).  idx: the event's place in the decoded sequence (its stream index,
+// or its place in a band's event list), the base of the chunk plus the lane.
 template <bool PAIR>
 __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c, int tv,
-                                           int sv, int j, int n_eff, int r0, int rn, int& oy0,
-                                           int& ox0, int32_t* cnt) {
+                                           int sv, int j, int idx, int n_eff, int r0, int rn,
+                                           int& oy0, int& ox0, int32_t* cnt) {
   const bool real = j < n_eff && sv >= 0;
   // source -> (channel, row, column); a source past the input is clamped into it (memory
   // safety only: the host rejects such ids)
@@ -340,7 +350,7 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
   const int slot = rel ? lanes_below(relm) : n + lanes_below(~relm);
   if (!PAIR) {
     c.rec[slot] = make_int4(tv, p0 * 4, q0 * 4, (int)(uint32_t)m);
-    c.rec1[slot] = make_int2((int)(uint32_t)(m >> 32), j);
+    c.rec1[slot] = make_int2((int)(uint32_t)(m >> 32), idx);
     return n;
   }
   // Pairs (candidate masks of 32 bits or less).  Two events whose candidate blocks are
@@ -377,45 +387,32 @@ __device__ __forceinline__ int conv_decode(const ConvGeom& g, const ConvLane& c,
   c.rec1[2 * lane + 1] = make_int2(0, -1);
   if (rel) {
     c.rec[rp] = make_int4(tv, p0 * 4, q0 * 4, (int)(uint32_t)m);
-    c.rec1[rp] = make_int2(0, j);
+    c.rec1[rp] = make_int2(0, idx);
   }
   return n - __popcll(seconds);
 }
 
-// Where a wave's spikes go.
-enum ConvMode { kStage = 0, kMask = 1 };
-
-// kMask: the spike-bit words in global memory of stream b.
-struct ConvSink {
-  int b;
-  uint32_t* masks;
-  int32_t* seg_cnt;  // this stream's row of per-segment spike counts
-  int L, OC, WPO, Gi;
-};
-
-// The events of one decoded chunk, in order (salt_core/quant/scan.py:22-52 per update).
-// kStage: stage the spike ballots for the work-group's merge; kMask: set spike bits in
-// global memory.  M32: candidate masks fit 32 bits (NC^2 <= 32).  NOTRUNC: no position
-// can hold max_queue_len events (max_queue_len >= the stream length), so every candidate
-// event is a real queue column.  PAIR: n_ev steps of two events, one per half-wave (a
-// step's second record covers nothing when it has one event).
-template <int NIT, bool SAT, bool EXT, bool VTHN, int MODE, bool M32, bool NOTRUNC, bool PAIR>
+// The events of one decoded chunk, in order (salt_core/quant/scan.py:22-52 per update),
+// with the spike ballots staged in LDS for the output (the work-group's merge, or the
+// spike words of a row band).  M32: candidate masks fit 32 bits (NC^2 <= 32).  NOTRUNC:
+// no position can hold max_queue_len events (max_queue_len >= the stream length), so
+// every candidate event is a real queue column.  PAIR: n_ev steps of two events, one per
+// half-wave (a step's second record covers nothing when it has one event).
+template <int NIT, bool SAT, bool EXT, bool VTHN, bool M32, bool NOTRUNC, bool PAIR>
 __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
                                             const int (&vtc)[NIT], int n_ev, int base,
-                                            const ConvSink& sk, int& vmin_l, int& vmax_l) {
+                                            int& vmin_l, int& vmax_l) {
   const int lane = threadIdx.x & (kWave - 1);
-  // kStage: the chunk's ballots and spike counts, indexed by the event's place in the
-  // chunk: events without a candidate in this sub-band keep "no spike".  These clears
-  // precede the events' entries (a wave's LDS writes complete in order).
-  if (MODE == kStage) {
+  // The chunk's ballots and spike counts, indexed by the event's place in the chunk:
+  // events without a candidate in this sub-band keep "no spike".  These clears precede
+  // the events' entries (a wave's LDS writes complete in order).
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) c.stg[lane * NIT + it] = ~0ull;
-    c.wcnt[lane] = 0;
-  }
+  for (int it = 0; it < NIT; ++it) c.stg[lane * NIT + it] = ~0ull;
+  c.wcnt[lane] = 0;
   if (n_ev == 0) return;
-  constexpr bool kRec1 = !M32 || MODE == kMask;  // the loop needs the second record word
-  // kStage: lane e of sg_lo/sg_hi[it] collects event e's spike ballot; they are
-  // stored once per chunk.
+  constexpr bool kRec1 = !M32;  // the loop needs the second record word
+  // lane e of sg_lo/sg_hi[it] collects event e's spike ballot; they are stored once per
+  // chunk.
   uint32_t sg_lo[NIT], sg_hi[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) { sg_lo[it] = ~0u; sg_hi[it] = ~0u; }
@@ -520,17 +517,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     int el = e;
     asm volatile("" : "+s"(el));
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      if (MODE == kStage) {
-        stage_to_lane(sg_lo[it], sg_hi[it], bal[it], el);
-      } else if (!((bal[it] >> lane) & 1)) {
-        // Bit = candidate index in the event's NC x NC grid (compaction decodes it).
-        const size_t w = ((size_t)sk.b * sk.L + r1.y) * (size_t)(sk.OC * sk.WPO) +
-                         (size_t)(c.oc_lane + it * sk.Gi) * sk.WPO + (c.cand >> 5);
-        atomicOr(&sk.masks[w], 1u << (c.cand & 31));
-        atomicAdd(&sk.seg_cnt[r1.y / kCompactSeg], 1);  // the compaction skips empty segments
-      }
-    }
+    for (int it = 0; it < NIT; ++it) stage_to_lane(sg_lo[it], sg_hi[it], bal[it], el);
     r = rn;
     r1 = rn1;
     vc = vcn;
@@ -567,7 +554,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     if (e < end) event(e++);
   }
   if (!PAIR) __builtin_amdgcn_s_setprio(3);
-  if (PAIR && MODE == kStage && lane < n_ev) {
+  if (PAIR && lane < n_ev) {
     // step lane: half-wave h's ballot bits belong to the event of record 2 * lane + h
     const int j0 = c.rec1[2 * lane].y - base, j1 = c.rec1[2 * lane + 1].y;
     int n0 = 0, n1 = 0;
@@ -583,7 +570,7 @@ __device__ __forceinline__ void conv_events(const Quant& qz, const ConvLane& c,
     c.wcnt[j0] = n0;
     if (j1 >= 0) c.wcnt[j1 - base] = n1;
   }
-  if (!PAIR && MODE == kStage && lane < n_ev) {
+  if (!PAIR && lane < n_ev) {
     const int jc = c.rec1[lane].y - base;  // the event's index within the chunk
     int nsp = 0;
 #pragma unroll
@@ -650,14 +637,19 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   // Wave wv serves stream slot ks of the work-group's spw streams, as its wave wl.
   const int nwps = a.ncg * a.nsb;
   const int ks = wv / nwps, wl = wv - ks * nwps;
-  const int b = blockIdx.y * a.spw + ks;
+  // Row-band plans: the bands of a stream read the same events, so they run on one XCD.
+  const int n_wg = gridDim.x * gridDim.y;
+  const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+  const int wg = a.merge ? lin : xcd_order(lin, n_wg);
+  const int bx = wg % gridDim.x, by = wg / gridDim.x;  // (band, group of streams)
+  const int b = by * a.spw + ks;
   const bool live = b < a.B;  // the last work-group's slots past the batch have no stream
   const int cg = wl % a.ncg, sb = wl / a.ncg;  // channel group, sub-band
   const int Gi = a.Gi, Gp = NIT * a.Gi;
   const int oc0 = cg * a.G;
   const int ocn = max(0, min(a.G, g.OC - oc0));
-  const int rows_end = min(g.H, (int)blockIdx.x * a.R + a.R);
-  const int r0 = blockIdx.x * a.R + sb * a.Rw;
+  const int rows_end = min(g.H, bx * a.R + a.R);
+  const int r0 = bx * a.R + sb * a.Rw;
   const int rn = max(0, min(a.Rw, rows_end - r0));
   const int W = g.W, Wp = g.Wp, PWs = a.Rw * Wp, PW = rn * W;
   const int ICKK = g.IC * g.K * g.K;
@@ -745,9 +737,6 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
 
   conv_lane_setup(c, g, lane, Gi, VS, QS, PWs, oc0, qz.n_table, NOTRUNC ? 4 : 8, smem, PAIR);
   int vtc[NIT];
-  ConvSink sk;
-  sk.b = b; sk.masks = a.masks; sk.L = a.L; sk.OC = g.OC; sk.WPO = a.WPO; sk.Gi = Gi;
-  sk.seg_cnt = a.seg_cnt ? a.seg_cnt + (size_t)min(b, a.B - 1) * a.nseg : nullptr;
 
   const int L = a.L;
   auto real_count = [&](int bi) {
@@ -759,7 +748,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int32_t* lst = nullptr;
   int n_list = 0;
   if (a.blist && live) {
-    const int bi = b * gridDim.x + blockIdx.x;
+    const int bi = b * gridDim.x + bx;
     n_list = __builtin_amdgcn_readfirstlane(a.bcnt[bi]);
     lst = a.blist + (size_t)b * a.bcap + a.boff[bi];
   }
@@ -770,7 +759,7 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     n_grp = n_list;
   } else {
     for (int i = lane; i < a.spw; i += kWave)
-      n_grp = max(n_grp, real_count(blockIdx.y * a.spw + i));
+      n_grp = max(n_grp, real_count(by * a.spw + i));
     n_grp = __builtin_amdgcn_readfirstlane(wave_max(n_grp));
   }
   const int nchunks = (n_grp + kWave - 1) / kWave;
@@ -803,11 +792,13 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
       s_n = sb_src[min(lane, jl)];
     }
   }
-  // Decoding wave: chunk k into record buffer k % 2 (and, merge mode, sub-band 0: the
-  // chunk's event times and plane positions into event buffer k % 3).
+  // Decoding wave: chunk k into record buffer k % 2 (and, sub-band 0, into event buffer
+  // k % 3: merge mode the chunk's event times and plane positions, row bands the events'
+  // stream indices).
   auto decode = [&](int k) {
     const int bf = k & 1;
-    int j = k * kWave + lane;
+    const int idx = k * kWave + lane;  // place in the stream or the band's list
+    int j = idx;
     const int tv = time_ms(t_n), sv = s_n;
     if (a.blist) {
       // list position -> original index (past the list: not real)
@@ -826,9 +817,34 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     c.rec = recs + bf * conv_recs(PAIR);
     c.rec1 = recs1 + bf * conv_recs(PAIR);
     int oy0 = 0, ox0 = 0;
-    const int n = conv_decode<PAIR>(g, c, tv, sv, j, n_eff, r0, rn, oy0, ox0, cnt_kept);
+    const int n = conv_decode<PAIR>(g, c, tv, sv, j, idx, n_eff, r0, rn, oy0, ox0, cnt_kept);
     if (lane == 0) nev[bf] = n;
-    if (a.merge && sb == 0) evt0[(k % kConvEvtBufs) * kWave + lane] = make_int2(tv, oy0 * W + ox0);
+    if (sb == 0)
+      evt0[(k % kConvEvtBufs) * kWave + lane] =
+          a.merge ? make_int2(tv, oy0 * W + ox0) : make_int2(j, 0);
+  };
+  // Row bands, every wave: for each event of chunk k with a spike in the band, its own
+  // spike words (all NIT, spikes or not) in the event's slot for this band; the first
+  // channel group marks the slot valid and adds the event's spikes in the band to its
+  // compaction segment.  Lane = the event's index in the chunk.
+  const int slot = bx % max(a.nslots, 1);
+  auto store_words = [&](int k) {
+    const int bf = k & 1;
+    int tot = 0;
+    for (int g2 = 0; g2 < a.ncg; ++g2)  // one sub-band per row band
+      tot += swave0[g2 * lay.wave_words + lay.wcnt + bf * kWave + lane];
+    if (tot == 0) return;
+    const int jj = evt0[(k % kConvEvtBufs) * kWave + lane].x;
+    const size_t ev = (size_t)b * L + jj;
+    uint64_t* const w = a.words + (ev * a.nslots + slot) * (size_t)(a.ncg * NIT) + cg * NIT;
+    const uint64_t* const kept =
+        reinterpret_cast<const uint64_t*>(wbase + lay.stg) + bf * kWave * NIT + lane * NIT;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) w[it] = ~kept[it];
+    if (cg == 0) {
+      atomicOr(&a.valid[ev], 1u << slot);
+      atomicAdd(&a.seg_cnt[(size_t)b * a.nseg + jj / kCompactSeg], tot);
+    }
   };
   // Merge mode, every wave: its own spikes of chunk k, at their places in the stream's
   // output, ordered (event, channel group, iteration, bit) = (event, ascending neuron id)
@@ -890,22 +906,23 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   for (int k = 0; k < nchunks; ++k) {
     const int bf = k & 1;
     if (dec && k + 1 < nchunks) decode(k + 1);
-    if (a.merge && k > 0) walk(k - 1);
+    if (k > 0) {
+      if (a.merge) walk(k - 1);
+      else if (live) store_words(k - 1);
+    }
     c.rec = recs + bf * conv_recs(PAIR);
     c.rec1 = recs1 + bf * conv_recs(PAIR);
     const int n_ev = __builtin_amdgcn_readfirstlane(nev[bf]);
-    if (a.merge) {
-      c.stg = stgs + bf * kWave * NIT;
-      c.wcnt = wbase + lay.wcnt + bf * kWave;
-      conv_events<NIT, SAT, EXT, VTHN, kStage, M32, NOTRUNC, PAIR>(qz, c, vtc, n_ev, k * kWave,
-                                                                         sk, vmin_l, vmax_l);
-    } else {
-      conv_events<NIT, SAT, EXT, VTHN, kMask, M32, NOTRUNC, PAIR>(qz, c, vtc, n_ev, k * kWave,
-                                                                        sk, vmin_l, vmax_l);
-    }
+    c.stg = stgs + bf * kWave * NIT;
+    c.wcnt = wbase + lay.wcnt + bf * kWave;
+    conv_events<NIT, SAT, EXT, VTHN, M32, NOTRUNC, PAIR>(qz, c, vtc, n_ev, k * kWave, vmin_l,
+                                                         vmax_l);
     __syncthreads();
   }
-  if (a.merge && nchunks > 0) walk(nchunks - 1);
+  if (nchunks > 0) {
+    if (a.merge) walk(nchunks - 1);
+    else if (live) store_words(nchunks - 1);
+  }
 
   const int T = n_eff > 0 ? time_ms(tb[n_eff - 1]) : 0;
   int maxcnt = 0;

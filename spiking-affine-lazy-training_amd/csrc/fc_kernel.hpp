@@ -181,20 +181,51 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
     if (__builtin_expect(__ballot(evt != 0) != 0, 0)) {  // readout layers rarely fire
       const int incl = wave_incl_scan(evt);
       const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
-      const float te = ms_time(tv);  // this lane's event time
-      int pos = out_base + incl - evt + lower;
+      // Lane = the chunk's event: this wave's spikes of it take places [first, first +
+      // cnt) of the chunk's output, which starts at out_base (places from cap on are
+      // dropped).
+      const int first = incl - evt + lower;
+      const int room = a.cap - out_base;
+      float* const ot = a.out_t + (size_t)b * a.cap + out_base;
+      int32_t* const os = a.out_s + (size_t)b * a.cap + out_base;
+      if (total > 2 * kWave) {
+        // Dense chunk: event by event with lane = neuron, so each store writes one run of
+        // consecutive entries (whole cache lines from one wave in quick succession)
+        // instead of one entry in each of 64 runs.  Measured on configuration 5 (~180
+        // spikes per event): 63.7 -> 42.0 ms, writes 110 -> 70 GB for 66 GB of entries.
+        const int te_bits = __float_as_int(ms_time(tv));
+        for (uint64_t evs = __ballot(cnt > 0); evs; evs &= evs - 1) {
+          const int e = __builtin_ctzll(evs);
+          int at = __builtin_amdgcn_readlane(first, e);
+          if (at >= room) break;  // so do the later events'
+          const float te = __int_as_float(__builtin_amdgcn_readlane(te_bits, e));
 #pragma unroll
-      for (int k = 0; k < NPL; ++k) {
-        uint64_t bits = sp[k];
-        while (bits) {
-          const int kb = __builtin_ctzll(bits);
-          bits &= bits - 1;
-          if (pos < a.cap) {
-            a.out_t[(size_t)b * a.cap + pos] = te;
-            a.out_s[(size_t)b * a.cap + pos] = n0 + k * kWave + kb;
+          for (int k = 0; k < NPL; ++k) {
+            const uint64_t m =
+                ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(sp[k] >> 32), e) << 32) |
+                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)sp[k], e);
+            const int r = at + (int)__builtin_amdgcn_mbcnt_hi(
+                                   (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            if (((m >> lane) & 1ull) && r < room) {
+              ot[r] = te;
+              os[r] = n0 + k * kWave + lane;
+            }
+            at += __popcll(m);
           }
-          ++pos;
         }
+      } else {
+        // Sparse chunk: each lane writes its event's run (a few stores in all).
+        const float te = ms_time(tv);
+        int pos = first;
+#pragma unroll
+        for (int k = 0; k < NPL; ++k)
+          for (uint64_t bits = sp[k]; bits; bits &= bits - 1) {
+            if (pos < room) {
+              ot[pos] = te;
+              os[pos] = n0 + k * kWave + __builtin_ctzll(bits);
+            }
+            ++pos;
+          }
       }
       out_base += total;
     }

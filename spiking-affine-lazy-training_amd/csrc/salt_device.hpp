@@ -18,6 +18,18 @@ constexpr int kWave = 64;
 constexpr int kCompactSeg = 2048;
 constexpr float kPadTime = 1e12f;  // salt_core/stream.py:13
 
+// MI355X hands the work-groups of a launch to its 8 XCDs in turn (linear id i to XCD
+// i % 8), and each XCD has an L2 of its own.  xcd_order(i, n) renumbers the n work-groups
+// so that each XCD runs one contiguous range of the new numbers: work-groups that read the
+// same data (the row bands of one stream) then fetch it into one L2 instead of eight.  A
+// bijection on [0, n); results never depend on it.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_order(int i, int n) {
+  const int q = n / kXcds, r = n - q * kXcds;
+  const int x = i % kXcds, k = i / kXcds;
+  return x * q + min(x, r) + k;
+}
+
 // Quantisation parameters of one layer, uniform over the launch.
 struct Quant {
   int fa;        // shift_bits of the decay multiply (f_a)

@@ -52,7 +52,10 @@ int32_t fail(int32_t code, const char* fmt, ...) {
       return fail(-2, "%s failed: %s", #expr, hipGetErrorString(e_));          \
   } while (0)
 
-constexpr int kLdsBandBudget = 64 * 1024;    // per band work-group: >= 2 fit a CU
+// LDS per row-band work-group: half a CU's, so two work-groups share a CU with bands as
+// tall as that allows (measured on configuration 4, conv kernel per launch: 52 KiB
+// 3.44 ms, 64 KiB 2.87 ms, 80 KiB 2.63 ms, 100 KiB 3.94 ms).
+constexpr int kLdsBandBudget = kLdsMax / 2;
 constexpr int kMaxTable = 1 << 20;           // decay-table entries (times stay exact)
 
 __global__ void fill_i32_kernel(int32_t* p, int32_t value, size_t n) {
@@ -63,12 +66,53 @@ __global__ void fill_i32_kernel(int32_t* p, int32_t value, size_t n) {
 
 // ------------------------------------------------------------------ compaction
 
+// Spikes -> ordered stream, in segments of kCompactSeg events so that a stream's walk and
+// its padding spread over many waves.  One wave per (segment, stream) starts its part of
+// the stream after the earlier segments' spikes, from per-segment spike counts (kept by
+// the conv kernel, or counted by compact_count_kernel for FC slices), and reads nothing
+// of a segment without spikes.  Walking the spikes of an event in ascending neuron id
+// gives the (event, neuron) order of salt_core/stream.py:24-46.
+
+int compact_segments(int L) { return std::max(1, (L + kCompactSeg - 1) / kCompactSeg); }
+
+__device__ __forceinline__ int stream_events(const int32_t* n_real, int b, int L) {
+  const int nr = n_real[b];
+  return nr < 0 ? 0 : (nr < L ? nr : L);
+}
+
+// Segment s's first place in stream b's output (before) and the stream's spike count.
+__device__ __forceinline__ void segment_start(const int32_t* seg_cnt, int b, int nseg, int s,
+                                              int& before, int& all) {
+  const int lane = threadIdx.x & (kWave - 1);
+  before = 0;
+  all = 0;
+  for (int t = lane; t < nseg; t += kWave) {
+    const int c = seg_cnt[b * nseg + t];
+    before += t < s ? c : 0;
+    all += c;
+  }
+  before = __builtin_amdgcn_readlane(wave_incl_scan(before), kWave - 1);
+  all = __builtin_amdgcn_readlane(wave_incl_scan(all), kWave - 1);
+}
+
+// The stream's count (by the last segment's wave) and its padding, shared by the
+// segments' waves: entries past the spikes hold (1e12, 0) when fill_pads.
+__device__ __forceinline__ void segment_finish(int b, int s, int nseg, int all, int cap,
+                                               int fill_pads, float* out_t, int32_t* out_s,
+                                               int32_t* out_n) {
+  const int lane = threadIdx.x & (kWave - 1);
+  if (s == nseg - 1 && lane == 0) out_n[b] = all;
+  if (fill_pads)
+    for (int i = min(all, cap) + s * kWave + lane; i < cap; i += nseg * kWave) {
+      out_t[(size_t)b * cap + i] = kPadTime;
+      out_s[(size_t)b * cap + i] = 0;
+    }
+}
+
+// FC slices: one bit per (event, neuron), words in neuron order (neuron = word*32 + bit).
 struct CompactArgs {
-  int conv;                      // 1: conv bit layout, 0: FC (neuron = word*32 + bit)
-  int words, WPO, NC, OC, HW, W, HWin, Win, K, S, P;
-  int L;
+  int words, L;
   const float* times;
-  const int32_t* src;
   const int32_t* n_real;
   const uint32_t* masks;
   int cap, fill_pads;
@@ -77,26 +121,14 @@ struct CompactArgs {
   int32_t* out_n;
 };
 
-// Spike bitmasks -> ordered stream, in segments of kCompactSeg events so that a stream's
-// walk and its padding spread over many waves: the per-segment spike counts come from
-// the layer kernel (conv: one atomic per spike) or compact_count_kernel (FC slices);
-// compact_kernel (one wave per segment) starts its part of the stream after the earlier
-// segments' spikes and reads no mask of a segment without spikes.  Words are in neuron
-// order and bits within a word too, so walking them gives the (event, neuron) order of
-// salt_core/stream.py:24-46.
-
-int compact_segments(int L) { return std::max(1, (L + kCompactSeg - 1) / kCompactSeg); }
-
 // Spikes per (stream, segment): the segment's mask words as one flat, coalesced array.
 __global__ void __launch_bounds__(64) compact_count_kernel(CompactArgs a, int32_t* seg_cnt,
                                                            int nseg) {
   const int lane = threadIdx.x;
   const int s = blockIdx.x, b = blockIdx.y;
-  const int L = a.L;
-  const int nr = a.n_real[b];
-  const int n_eff = nr < 0 ? 0 : (nr < L ? nr : L);
+  const int n_eff = stream_events(a.n_real, b, a.L);
   const int j0 = min(n_eff, s * kCompactSeg), j1 = min(n_eff, j0 + kCompactSeg);
-  const uint32_t* m = a.masks + ((size_t)b * L + j0) * a.words;
+  const uint32_t* m = a.masks + ((size_t)b * a.L + j0) * a.words;
   const size_t nw = (size_t)(j1 - j0) * a.words;
   int cnt = 0;
   for (size_t i = lane; i < nw; i += kWave) cnt += __popc(m[i]);
@@ -104,23 +136,15 @@ __global__ void __launch_bounds__(64) compact_count_kernel(CompactArgs a, int32_
   if (lane == 0) seg_cnt[b * nseg + s] = total;
 }
 
-// One wave per (segment, stream); lane = event within a chunk of 64.
+// One wave per (segment, stream); lane = event within a window of 64.
 __global__ void __launch_bounds__(64) compact_kernel(CompactArgs a, const int32_t* seg_cnt,
                                                      int nseg) {
   const int lane = threadIdx.x;
   const int s = blockIdx.x, b = blockIdx.y;
   const int L = a.L;
-  const int nr = a.n_real[b];
-  const int n_eff = nr < 0 ? 0 : (nr < L ? nr : L);
-  // this segment's first place in the stream, and the stream's spike count
-  int before = 0, all = 0;
-  for (int t = lane; t < nseg; t += kWave) {
-    const int c = seg_cnt[b * nseg + t];
-    before += t < s ? c : 0;
-    all += c;
-  }
-  before = __builtin_amdgcn_readlane(wave_incl_scan(before), kWave - 1);
-  all = __builtin_amdgcn_readlane(wave_incl_scan(all), kWave - 1);
+  const int n_eff = stream_events(a.n_real, b, L);
+  int before, all;
+  segment_start(seg_cnt, b, nseg, s, before, all);
   int out_base = before;
   const int j_end = seg_cnt[b * nseg + s] > 0 ? min(n_eff, (s + 1) * kCompactSeg) : 0;
   for (int base = s * kCompactSeg; base < j_end; base += kWave) {
@@ -131,36 +155,86 @@ __global__ void __launch_bounds__(64) compact_kernel(CompactArgs a, const int32_
     if (ok)
       for (int w = 0; w < a.words; ++w) count += __popc(m[w]);
     const int incl = wave_incl_scan(count);
-    const int excl = incl - count;
     const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
     if (ok && count > 0) {
-      int pos = out_base + excl;
+      int pos = out_base + incl - count;
       const float te = a.times[(size_t)b * L + j];
-      int oy0 = 0, ox0 = 0;
-      if (a.conv) {
-        const int sv = a.src[(size_t)b * L + j];
-        const int rem = sv % a.HWin;
-        const int y = rem / a.Win, x = rem - (rem / a.Win) * a.Win;
-        oy0 = floordiv_pos(y + a.P - a.K + a.S, a.S);
-        ox0 = floordiv_pos(x + a.P - a.K + a.S, a.S);
-      }
-      for (int w = 0; w < a.words; ++w) {
-        uint32_t bits = m[w];
-        while (bits) {
-          const int bit = __builtin_ctz(bits);
-          bits &= bits - 1;
-          int neuron;
-          if (a.conv) {
-            const int oc = w / a.WPO;
-            const int r = (w - oc * a.WPO) * 32 + bit;
-            const int dy = r / a.NC, dx = r - (r / a.NC) * a.NC;
-            neuron = oc * a.HW + (oy0 + dy) * a.W + (ox0 + dx);
-          } else {
-            neuron = w * 32 + bit;
-          }
+      for (int w = 0; w < a.words; ++w)
+        for (uint32_t bits = m[w]; bits; bits &= bits - 1) {
           if (pos < a.cap) {
             a.out_t[(size_t)b * a.cap + pos] = te;
-            a.out_s[(size_t)b * a.cap + pos] = neuron;
+            a.out_s[(size_t)b * a.cap + pos] = w * 32 + __builtin_ctz(bits);
+          }
+          ++pos;
+        }
+    }
+    out_base += total;
+  }
+  segment_finish(b, s, nseg, all, a.cap, a.fill_pads, a.out_t, a.out_s, a.out_n);
+}
+
+// Conv row bands: the spike words of conv_layer_kernel (per event, one slot per band it
+// reaches, valid bits telling which slots were stored).  Word (g, it) of a slot holds, at
+// bit l, channel g*G + it*Gi + l / NC2 and candidate l % NC2 of the event's NC x NC grid;
+// the slots of one event cover disjoint candidate rows, so a channel's candidates are the
+// union of its bits over the stored slots.
+struct BandCompactArgs {
+  int L, HW, W, HWin, Win, K, S, P, NC, NC2, OC;
+  int G, Gi, nit, ncg, nslots;
+  const float* times;
+  const int32_t* src;
+  const int32_t* n_real;
+  const uint64_t* words;
+  const uint32_t* valid;
+  int cap, fill_pads;
+  float* out_t;
+  int32_t* out_s;
+  int32_t* out_n;
+};
+
+// One wave per (segment, stream); lane = event within a window of 64.
+__global__ void __launch_bounds__(64) band_compact_kernel(BandCompactArgs a,
+                                                          const int32_t* seg_cnt, int nseg) {
+  const int lane = threadIdx.x;
+  const int s = blockIdx.x, b = blockIdx.y;
+  const int L = a.L;
+  const int n_eff = stream_events(a.n_real, b, L);
+  int before, all;
+  segment_start(seg_cnt, b, nseg, s, before, all);
+  int out_base = before;
+  const int wpe = a.ncg * a.nit;  // words per (event, slot)
+  const uint64_t cand_mask = a.NC2 >= 64 ? ~0ull : (1ull << a.NC2) - 1;
+  const int j_end = seg_cnt[b * nseg + s] > 0 ? min(n_eff, (s + 1) * kCompactSeg) : 0;
+  for (int base = s * kCompactSeg; base < j_end; base += kWave) {
+    const int j = base + lane;
+    const size_t ev = (size_t)b * L + j;
+    const uint32_t vb = j < j_end ? a.valid[ev] : 0u;
+    const uint64_t* const wv = a.words + ev * a.nslots * wpe;
+    int count = 0;
+    for (int sl = 0; sl < a.nslots; ++sl)
+      if ((vb >> sl) & 1u)
+        for (int w = 0; w < wpe; ++w) count += __popcll(wv[sl * wpe + w]);
+    const int incl = wave_incl_scan(count);
+    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+    if (count > 0) {
+      int pos = out_base + incl - count;
+      const float te = a.times[ev];
+      const int rem = a.src[ev] % a.HWin;
+      const int y = rem / a.Win, x = rem - (rem / a.Win) * a.Win;
+      const int oy0 = floordiv_pos(y + a.P - a.K + a.S, a.S);
+      const int ox0 = floordiv_pos(x + a.P - a.K + a.S, a.S);
+      for (int oc = 0; oc < a.OC; ++oc) {
+        const int g = oc / a.G, sc = oc - g * a.G, it = sc / a.Gi;
+        const int wi = g * a.nit + it, sh = (sc - it * a.Gi) * a.NC2;
+        uint64_t m = 0;
+        for (int sl = 0; sl < a.nslots; ++sl)
+          if ((vb >> sl) & 1u) m |= wv[sl * wpe + wi] >> sh;
+        for (m &= cand_mask; m; m &= m - 1) {
+          const int r = __builtin_ctzll(m);
+          const int dy = r / a.NC, dx = r - (r / a.NC) * a.NC;
+          if (pos < a.cap) {
+            a.out_t[(size_t)b * a.cap + pos] = te;
+            a.out_s[(size_t)b * a.cap + pos] = oc * a.HW + (oy0 + dy) * a.W + (ox0 + dx);
           }
           ++pos;
         }
@@ -168,12 +242,7 @@ __global__ void __launch_bounds__(64) compact_kernel(CompactArgs a, const int32_
     }
     out_base += total;
   }
-  if (s == nseg - 1 && lane == 0) a.out_n[b] = all;
-  if (a.fill_pads)  // the segments share the padding
-    for (int i = min(all, a.cap) + s * kWave + lane; i < a.cap; i += nseg * kWave) {
-      a.out_t[(size_t)b * a.cap + i] = kPadTime;
-      a.out_s[(size_t)b * a.cap + i] = 0;
-    }
+  segment_finish(b, s, nseg, all, a.cap, a.fill_pads, a.out_t, a.out_s, a.out_n);
 }
 
 // ------------------------------------------------------------------ row-band event lists
@@ -182,18 +251,30 @@ __global__ void __launch_bounds__(64) compact_kernel(CompactArgs a, const int32_
 // rows [ceil((y+P-K+1)/S), floor((y+P)/S)] meet the band (the decode's row test; it
 // keeps a superset of the events with a candidate there), as original indices in order,
 // so that a band's work-group decodes its events alone instead of the whole stream.
+// Three small kernels, each event read once per pass: band_count_kernel counts the
+// events of every band per segment of kBandSeg events, band_scan_kernel turns the counts
+// into list positions, band_fill_kernel writes the lists.
+constexpr int kBandSeg = 1024;    // events per segment of the list build
+constexpr int kBandMaxRb = 4096;  // bands per stream with lists (LDS of the list build)
+static_assert(kBandMaxRb * 12 <= 64 * 1024, "band_fill_kernel's LDS");
+
 struct BandArgs {
-  int L, R, H, n_rb, K, S, P, HWin, Win, n_src, cap;
-  float rHWin, rWin, rS;
+  int L, R, H, n_rb, K, S, P, HWin, Win, n_src, cap, nseg;
+  float rHWin, rWin, rS, rR;
   const int32_t* src;
   const int32_t* n_real;
-  int32_t* cnt;   // [B][n_rb]
-  int32_t* off;   // [B][n_rb]: first entry of the band's list in the stream's region
-  int32_t* list;  // [B][cap]
+  int32_t* cnt;      // [B][n_rb]: events in the band's list
+  int32_t* off;      // [B][n_rb]: first entry of the band's list in the stream's region
+  int32_t* list;     // [B][cap]
+  int32_t* seg_pos;  // [B][nseg][n_rb]: counts per segment, then the segment's first places
 };
 
-// Whether source s (an input pixel) has candidate rows in [r0, r1).
-__device__ __forceinline__ bool band_meets(const BandArgs& a, int s, int r0, int r1) {
+// The bands [b0, b1] that source s (an input pixel) reaches: its candidate rows clipped to
+// the plane, in bands of R rows; b1 < b0 when it reaches none (s < 0: no event).
+__device__ __forceinline__ void band_range(const BandArgs& a, int s, int& b0, int& b1) {
+  b0 = 0;
+  b1 = -1;
+  if (s < 0) return;
   s = min(s, a.n_src - 1);
   int ch, y, lo, hi;
   if (a.n_src <= (1 << 22)) {
@@ -207,44 +288,128 @@ __device__ __forceinline__ bool band_meets(const BandArgs& a, int s, int r0, int
     lo = floordiv_pos(y + a.P - a.K + a.S, a.S);
     hi = (y + a.P) / a.S;
   }
-  return max(lo, r0) <= min(hi, r1 - 1);
+  lo = max(lo, 0);
+  hi = min(hi, a.H - 1);
+  if (lo > hi) return;
+  b0 = div_small(lo, a.R, a.rR);
+  b1 = div_small(hi, a.R, a.rR);
 }
 
-// One wave per (band, stream): blockIdx.x = band.  PASS 0 counts the band's events;
-// PASS 1 writes them at the band's offset (the stream's earlier bands' counts).  Four
-// windows of 64 events per iteration keep four loads in flight.
-template <int PASS>
-__global__ void __launch_bounds__(64) band_list_kernel(BandArgs a) {
+__device__ __forceinline__ int band_events(const BandArgs& a, int b) {
+  return stream_events(a.n_real, b, a.L);
+}
+
+// One wave per (segment, stream): the segment's events per band.
+__global__ void __launch_bounds__(64) band_count_kernel(BandArgs a) {
+  __shared__ int32_t hist[kBandMaxRb];
   const int lane = threadIdx.x;
-  const int rb = blockIdx.x, b = blockIdx.y;
-  const int nr = a.n_real[b];
-  const int n_eff = nr < 0 ? 0 : (nr < a.L ? nr : a.L);
-  const int r0 = rb * a.R, r1 = min(a.H, r0 + a.R);
+  const int sg = blockIdx.x, b = blockIdx.y;
+  for (int i = lane; i < a.n_rb; i += kWave) hist[i] = 0;
+  __syncthreads();
+  const int j0 = sg * kBandSeg, j1 = min(band_events(a, b), j0 + kBandSeg);
   const int32_t* src = a.src + (size_t)b * a.L;
-  int pos = 0;
-  if (PASS == 1) {
-    for (int t = lane; t < rb; t += kWave) pos += a.cnt[b * a.n_rb + t];
-    pos = __builtin_amdgcn_readlane(wave_incl_scan(pos), kWave - 1);
-    if (lane == 0) a.off[b * a.n_rb + rb] = pos;
+  for (int base = j0; base < j1; base += kWave) {
+    const int j = base + lane;
+    int b0, b1;
+    band_range(a, j < j1 ? src[j] : -1, b0, b1);
+    for (int k = b0; k <= b1; ++k) atomicAdd(&hist[k], 1);
   }
+  __syncthreads();
+  int32_t* const out = a.seg_pos + ((size_t)b * a.nseg + sg) * a.n_rb;
+  for (int i = lane; i < a.n_rb; i += kWave) out[i] = hist[i];
+}
+
+// One wave per stream, lane = band: each band's list length and offset (its stream's
+// earlier bands' lengths), then each segment's first place in the band's list.
+__global__ void __launch_bounds__(64) band_scan_kernel(BandArgs a) {
+  const int lane = threadIdx.x;
+  const int b = blockIdx.x;
+  int32_t* const rows = a.seg_pos + (size_t)b * a.nseg * a.n_rb;
+  constexpr int kBatch = 8;  // loads in flight per lane
+  int run = 0;
+  for (int rb0 = 0; rb0 < a.n_rb; rb0 += kWave) {
+    const int rb = rb0 + lane;
+    const bool ok = rb < a.n_rb;
+    int tot = 0;
+    for (int s0 = 0; s0 < a.nseg; s0 += kBatch) {
+      int c[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        c[u] = (ok && s0 + u < a.nseg) ? rows[(size_t)(s0 + u) * a.n_rb + rb] : 0;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) tot += c[u];
+    }
+    const int incl = wave_incl_scan(tot);
+    int pos = run + incl - tot;
+    if (ok) {
+      a.cnt[b * a.n_rb + rb] = tot;
+      a.off[b * a.n_rb + rb] = pos;
+    }
+    run += __builtin_amdgcn_readlane(incl, kWave - 1);
+    for (int s0 = 0; s0 < a.nseg; s0 += kBatch) {
+      int c[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        c[u] = (ok && s0 + u < a.nseg) ? rows[(size_t)(s0 + u) * a.n_rb + rb] : 0;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (ok && s0 + u < a.nseg) rows[(size_t)(s0 + u) * a.n_rb + rb] = pos;
+        pos += c[u];
+      }
+    }
+  }
+}
+
+// One wave per (segment, stream): the segment's events appended to the lists of the
+// bands they reach.  Per window of 64 events (lane = event): every lane marks its bit in
+// the lane set of each band it reaches (an LDS OR), so that a lane's place in a band's
+// list is the band's next place plus the lanes below it in the band's set; the lowest
+// lane of each set then advances the band's next place and clears the set.  nslots:
+// bands one event reaches at most.  LDS: n_rb lane sets (8 bytes) and next places.
+__global__ void __launch_bounds__(64) band_fill_kernel(BandArgs a, int nslots) {
+  extern __shared__ int32_t bsm[];
+  uint64_t* const lanes_of = reinterpret_cast<uint64_t*>(bsm);
+  int32_t* const next = bsm + 2 * a.n_rb;
+  const int lane = threadIdx.x;
+  // The segments of a stream run on one XCD: their partial lines of a band's list then
+  // meet in one L2 before they reach HBM.
+  const int wg = xcd_order(blockIdx.y * gridDim.x + blockIdx.x, gridDim.x * gridDim.y);
+  const int sg = wg % gridDim.x, b = wg / gridDim.x;
+  const int32_t* pos = a.seg_pos + ((size_t)b * a.nseg + sg) * a.n_rb;
+  for (int i = lane; i < a.n_rb; i += kWave) {
+    next[i] = pos[i];
+    lanes_of[i] = 0;
+  }
+  __syncthreads();
+  const int j0 = sg * kBandSeg, j1 = min(band_events(a, b), j0 + kBandSeg);
+  const int32_t* src = a.src + (size_t)b * a.L;
   int32_t* const out = a.list + (size_t)b * a.cap;
-  for (int base = 0; base < n_eff; base += 4 * kWave) {
-    int sv[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int j = base + u * kWave + lane;
-      sv[u] = j < n_eff ? src[j] : -1;
+  const uint64_t below = (1ull << lane) - 1;
+  for (int base = j0; base < j1; base += kWave) {
+    const int j = base + lane;
+    int b0, b1;
+    band_range(a, j < j1 ? src[j] : -1, b0, b1);
+    for (int k = 0; k < nslots; ++k)
+      if (b0 + k <= b1) atomicOr(reinterpret_cast<unsigned long long*>(&lanes_of[b0 + k]),
+                                 1ull << lane);
+    __syncthreads();
+    uint32_t lead = 0;  // bit k: this lane is the lowest of band b0 + k's set
+    for (int k = 0; k < nslots; ++k) {
+      if (b0 + k > b1) continue;
+      const uint64_t m = lanes_of[b0 + k];
+      const int at = next[b0 + k];
+      out[at + __popcll(m & below)] = j;
+      lead |= (m & below) == 0 ? 1u << k : 0u;
     }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int j = base + u * kWave + lane;
-      const bool in = sv[u] >= 0 && band_meets(a, sv[u], r0, r1);
-      const uint64_t m = __ballot(in);
-      if (PASS == 1 && in) out[pos + lanes_below(m)] = j;
-      pos += __popcll(m);
+    __syncthreads();
+    for (int k = 0; k < nslots; ++k) {
+      if (!((lead >> k) & 1)) continue;
+      const int bk = b0 + k;
+      next[bk] += __popcll(lanes_of[bk]);
+      lanes_of[bk] = 0;
     }
+    __syncthreads();
   }
-  if (PASS == 0 && lane == 0) a.cnt[b * a.n_rb + rb] = pos;
 }
 
 // ------------------------------------------------------------------ hash
@@ -301,7 +466,7 @@ __global__ void transpose_kernel(const T* in, T* out, int n_out, int n_in) {
 // ------------------------------------------------------------------ planning
 
 struct ConvPlan {
-  int H, W, HW, NC, NC2, WPO, Gi, G, nit, ncg, nsb, Rw, R, n_rb, merge, spw;
+  int H, W, HW, NC, NC2, Gi, G, nit, ncg, nsb, Rw, R, n_rb, merge, spw;
   int Wp, VS, QS;  // LDS row stride and slot strides (choose_layout)
   int tsplit;      // no queue truncation possible: times and counts in separate arrays
   int pair;        // two events per step, one per half-wave (NC2 <= 32)
@@ -463,6 +628,13 @@ bool plan_override(int* ncg_max, int* nsb) {
   return e && sscanf(e, "%d,%d", ncg_max, nsb) == 2 && *ncg_max >= 1 && *nsb >= 1;
 }
 
+// LDS per row-band work-group: kLdsBandBudget, or SALT_CONV_BAND_KB=n KiB (tuning runs).
+size_t band_budget() {
+  const char* e = getenv("SALT_CONV_BAND_KB");
+  const int kb = e ? atoi(e) : 0;
+  return kb > 0 ? std::min<size_t>((size_t)kb << 10, kLdsMax) : (size_t)kLdsBandBudget;
+}
+
 // SALT_CONV_PAIR=0 / =1 forces steps of one / two events (where candidates fit half a
 // wave) for comparisons and tests; both give the same results.  -1: not forced.
 int pair_override() {
@@ -530,7 +702,6 @@ int32_t plan_conv_mode(const salt_layer_desc* d, const salt_qparams* p, int B, b
   if (pl->NC2 > kWave)
     return fail(-3, "conv: %d candidate positions per event (k=%d, s=%d) exceed 64", pl->NC2,
                 d->k, d->s);
-  pl->WPO = (pl->NC2 + 31) / 32;
   pl->pair = pair && pl->NC2 <= kWave / 2 ? 1 : 0;
   pl->Gi = (pl->pair ? kWave / 2 : kWave) / pl->NC2;  // slots per (half-)wave
   const int H = pl->H, OC = d->oc;
@@ -552,18 +723,19 @@ int32_t plan_conv_mode(const salt_layer_desc* d, const salt_qparams* p, int B, b
   }
   // Bands of rows, one work-group (of channel-group waves) each, within the budget.
   pl->nsb = 1; pl->merge = 0;
+  const size_t budget = band_budget();
   int R = H;
   for (;;) {
     pl->Rw = pl->R = R;
     default_layout(d, pl);
     pl->lds = conv_lds_bytes(d, p, *pl, ext);
-    if (pl->lds <= (size_t)kLdsBandBudget || R == 1) break;
+    if (pl->lds <= budget || R == 1) break;
     --R;
   }
   if (pl->lds > (size_t)kLdsMax)
     return fail(-3, "conv: one output row does not fit in LDS (w_out=%d)", pl->W);
   pl->n_rb = (H + R - 1) / R;
-  choose_layout(d, p, ext, std::max(pl->lds, (size_t)kLdsBandBudget), pl);
+  choose_layout(d, p, ext, std::max(pl->lds, budget), pl);
   return 0;
 }
 
@@ -771,52 +943,57 @@ ConvGeom conv_geom(const salt_layer_desc* d, const ConvPlan& pl) {
   return g;
 }
 
-// Workspace of a compacted layer: the spike masks, then (256-byte aligned) the spikes per
-// (stream, segment) of the compaction.
+// Workspace of a compacted layer: the spikes (FC slices: bit masks; conv row bands: the
+// validity words, then the spike words), then (256-byte aligned) the spikes per (stream,
+// segment) of the compaction.
 size_t masks_end(size_t mask_bytes) { return (mask_bytes + 255) & ~(size_t)255; }
 size_t compact_bytes(size_t mask_bytes, int B, int L) {
   return masks_end(mask_bytes) + (size_t)B * compact_segments(L) * 4;
 }
-size_t mask_only_conv(const ConvPlan& pl, const salt_layer_desc* d, int B, int L) {
-  return (size_t)B * L * d->oc * pl.WPO * 4;
+// Bands an event reaches at most: its NC candidate rows meet ceil((NC-1)/R) + 1 bands.
+int band_slots(const ConvPlan& pl) { return (pl.NC - 1 + pl.R - 1) / pl.R + 1; }
+size_t valid_bytes_conv(int B, int L) { return masks_end((size_t)B * L * 4); }
+size_t spike_bytes_conv(const ConvPlan& pl, int B, int L) {
+  return valid_bytes_conv(B, L) + (size_t)B * L * band_slots(pl) * pl.ncg * pl.nit * 8;
 }
-// Row-band event lists (band_list_kernel): entries per stream, as an event's candidate
-// rows (NC of them) meet at most ceil((NC-1)/R) + 1 bands of R rows; 0 when lists are
-// off (SALT_CONV_BANDLIST=0, for comparisons) or would not fit 32-bit indices.
+// Row-band event lists (band_count/scan/fill_kernel): entries per stream, one per band an
+// event reaches; 0 when lists are off (SALT_CONV_BANDLIST=0, for comparisons), the bands
+// exceed the list build's LDS or the entries would not fit 32-bit indices.
 long band_cap(const ConvPlan& pl, int L) {
   const char* e = getenv("SALT_CONV_BANDLIST");
-  if (pl.merge || (e && e[0] == '0')) return 0;
-  const long cap = (long)L * ((pl.NC - 1 + pl.R - 1) / pl.R + 1);
+  if (pl.merge || pl.n_rb > kBandMaxRb || (e && e[0] == '0')) return 0;
+  const long cap = (long)L * band_slots(pl);
   return cap <= INT_MAX ? cap : 0;
 }
+int band_segments(int L) { return std::max(1, (L + kBandSeg - 1) / kBandSeg); }
+// lengths and offsets, the lists, the per-segment places
 size_t band_bytes(const ConvPlan& pl, int B, int L) {
   const long cap = band_cap(pl, L);
-  return cap ? (size_t)B * pl.n_rb * 2 * 4 + (size_t)B * cap * 4 : 0;
+  return cap ? (size_t)B * pl.n_rb * 2 * 4 + (size_t)B * cap * 4 +
+                   (size_t)B * band_segments(L) * pl.n_rb * 4
+             : 0;
 }
-size_t mask_bytes_conv(const ConvPlan& pl, const salt_layer_desc* d, int B, int L) {
+size_t mask_bytes_conv(const ConvPlan& pl, int B, int L) {
   if (pl.merge) return 0;
-  return masks_end(compact_bytes(mask_only_conv(pl, d, B, L), B, L)) + band_bytes(pl, B, L);
+  return masks_end(compact_bytes(spike_bytes_conv(pl, B, L), B, L)) + band_bytes(pl, B, L);
 }
 size_t mask_only_fc(const FcPlan& pl, int B, int L) { return (size_t)B * L * pl.words * 4; }
 size_t mask_bytes_fc(const FcPlan& pl, int B, int L) {
   return pl.direct ? 0 : compact_bytes(mask_only_fc(pl, B, L), B, L);
 }
 
-// Launches the two compaction kernels over a layer's spike masks.
-// counted: the layer kernel has already summed each segment's spikes.
 int32_t* compact_seg_counts(void* ws, size_t mask_bytes) {
   return reinterpret_cast<int32_t*>(static_cast<char*>(ws) + masks_end(mask_bytes));
 }
 
+// Launches the two compaction kernels over an FC layer's spike masks.
 int32_t launch_compact(const CompactArgs& c, int B, int L, size_t mask_bytes, void* ws,
-                       hipStream_t st, bool counted = false) {
+                       hipStream_t st) {
   const int nseg = compact_segments(L);
   int32_t* const seg = compact_seg_counts(ws, mask_bytes);
   const dim3 grid(nseg, B);
-  if (!counted) {
-    hipLaunchKernelGGL(compact_count_kernel, grid, dim3(kWave), 0, st, c, seg, nseg);
-    HIP_TRY(hipGetLastError());
-  }
+  hipLaunchKernelGGL(compact_count_kernel, grid, dim3(kWave), 0, st, c, seg, nseg);
+  HIP_TRY(hipGetLastError());
   hipLaunchKernelGGL(compact_kernel, grid, dim3(kWave), 0, st, c, (const int32_t*)seg, nseg);
   HIP_TRY(hipGetLastError());
   return 0;
@@ -921,15 +1098,14 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     ConvPlan pl;
     rc = plan_conv(desc, prm, B, ext, notrunc, &pl);
     if (rc) return rc;
-    const size_t need = mask_bytes_conv(pl, desc, B, L);
+    const size_t need = mask_bytes_conv(pl, B, L);
     if (workspace_bytes < need || (need && !d_workspace))
       return fail(-1, "workspace of %zu bytes below the %zu needed", workspace_bytes, need);
     if (!launch) return 0;
     choose_spw(desc, prm, B, ext, &pl);
     ConvArgs a;
-    a.seg_cnt = nullptr; a.nseg = 0;  // set for mask plans below
+    a.seg_cnt = nullptr; a.nseg = 0;  // row bands: set below
     a.g = conv_geom(desc, pl);
-    a.WPO = pl.WPO;
     a.G = pl.G; a.Gi = pl.Gi; a.ncg = pl.ncg; a.nsb = pl.nsb; a.Rw = pl.Rw; a.R = pl.R;
     a.spw = pl.spw; a.B = B;
     a.VS = pl.VS; a.QS = pl.QS;
@@ -939,33 +1115,40 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     a.out_t = out->d_times; a.out_s = out->d_src; a.out_n = out->d_n;
     a.v_final = res->d_v_final; a.v_min = res->d_v_min; a.v_max = res->d_v_max;
     a.stats = res->d_stats;
-    a.masks = static_cast<uint32_t*>(d_workspace);
+    // row bands: validity words, spike words, segment counts, event lists
+    a.valid = static_cast<uint32_t*>(d_workspace);
+    a.words = reinterpret_cast<uint64_t*>(static_cast<char*>(d_workspace) +
+                                          valid_bytes_conv(B, L));
+    a.nslots = pl.merge ? 0 : band_slots(pl);
     a.blist = nullptr; a.bcnt = nullptr; a.boff = nullptr; a.bcap = 0;
     if (const long cap = band_cap(pl, L)) {  // row bands: each band's events, listed
       BandArgs ba;
       ba.L = L; ba.R = pl.R; ba.H = pl.H; ba.n_rb = pl.n_rb; ba.K = desc->k; ba.S = desc->s;
       ba.P = desc->p; ba.HWin = a.g.HWin; ba.Win = desc->w_in; ba.n_src = desc->ic * a.g.HWin;
-      ba.cap = (int)cap; ba.rHWin = a.g.rHWin; ba.rWin = a.g.rWin; ba.rS = a.g.rS;
+      ba.cap = (int)cap; ba.nseg = band_segments(L);
+      ba.rHWin = a.g.rHWin; ba.rWin = a.g.rWin; ba.rS = a.g.rS; ba.rR = 1.0f / (float)pl.R;
       ba.src = in->d_src; ba.n_real = in->d_n_real;
       ba.cnt = reinterpret_cast<int32_t*>(
           static_cast<char*>(d_workspace) +
-          masks_end(compact_bytes(mask_only_conv(pl, desc, B, L), B, L)));
+          masks_end(compact_bytes(spike_bytes_conv(pl, B, L), B, L)));
       ba.off = ba.cnt + (size_t)B * pl.n_rb;
       ba.list = ba.off + (size_t)B * pl.n_rb;
-      const dim3 bgrid(pl.n_rb, B);
-      hipLaunchKernelGGL(band_list_kernel<0>, bgrid, dim3(kWave), 0, st, ba);
+      ba.seg_pos = ba.list + (size_t)B * cap;
+      const dim3 sgrid(ba.nseg, B);
+      hipLaunchKernelGGL(band_count_kernel, sgrid, dim3(kWave), 0, st, ba);
       HIP_TRY(hipGetLastError());
-      hipLaunchKernelGGL(band_list_kernel<1>, bgrid, dim3(kWave), 0, st, ba);
+      hipLaunchKernelGGL(band_scan_kernel, dim3(B), dim3(kWave), 0, st, ba);
+      HIP_TRY(hipGetLastError());
+      hipLaunchKernelGGL(band_fill_kernel, sgrid, dim3(kWave), (size_t)pl.n_rb * 12, st, ba,
+                         band_slots(pl));
       HIP_TRY(hipGetLastError());
       a.blist = ba.list; a.bcnt = ba.cnt; a.boff = ba.off; a.bcap = ba.cap;
     }
     if (!pl.merge) {
       if ((rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
-      if ((rc = fill(reinterpret_cast<int32_t*>(a.masks), 0,
-                     mask_only_conv(pl, desc, B, L) / 4, st)))
-        return rc;
+      if ((rc = fill(reinterpret_cast<int32_t*>(a.valid), 0, (size_t)B * L, st))) return rc;
       a.nseg = compact_segments(L);
-      a.seg_cnt = compact_seg_counts(d_workspace, mask_only_conv(pl, desc, B, L));
+      a.seg_cnt = compact_seg_counts(d_workspace, spike_bytes_conv(pl, B, L));
       if ((rc = fill(a.seg_cnt, 0, (size_t)B * a.nseg, st))) return rc;
     }
     const int flags = (sat ? kConvSat : 0) | (ext ? kConvExt : 0) |
@@ -975,16 +1158,17 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
                       (pl.pair ? kConvPair : 0);
     HIP_TRY(launch_conv(a, pl, flags, B, st));
     if (!pl.merge) {
-      CompactArgs c;
-      c.conv = 1; c.words = desc->oc * pl.WPO; c.WPO = pl.WPO; c.NC = pl.NC; c.OC = desc->oc;
-      c.HW = pl.HW; c.W = pl.W; c.HWin = a.g.HWin; c.Win = desc->w_in; c.K = desc->k;
-      c.S = desc->s; c.P = desc->p; c.L = L; c.times = in->d_times; c.src = in->d_src;
-      c.n_real = in->d_n_real; c.masks = a.masks; c.cap = out->cap;
-      c.fill_pads = out->fill_pads; c.out_t = out->d_times; c.out_s = out->d_src;
-      c.out_n = out->d_n;
-      if ((rc = launch_compact(c, B, L, mask_only_conv(pl, desc, B, L), d_workspace, st,
-                               /*counted=*/true)))
-        return rc;
+      BandCompactArgs c;
+      c.L = L; c.HW = pl.HW; c.W = pl.W; c.HWin = a.g.HWin; c.Win = desc->w_in; c.K = desc->k;
+      c.S = desc->s; c.P = desc->p; c.NC = pl.NC; c.NC2 = pl.NC2; c.OC = desc->oc;
+      c.G = pl.G; c.Gi = pl.Gi; c.nit = pl.nit; c.ncg = pl.ncg; c.nslots = a.nslots;
+      c.times = in->d_times; c.src = in->d_src; c.n_real = in->d_n_real;
+      c.words = a.words; c.valid = a.valid;
+      c.cap = out->cap; c.fill_pads = out->fill_pads;
+      c.out_t = out->d_times; c.out_s = out->d_src; c.out_n = out->d_n;
+      hipLaunchKernelGGL(band_compact_kernel, dim3(a.nseg, B), dim3(kWave), 0, st, c,
+                         (const int32_t*)a.seg_cnt, a.nseg);
+      HIP_TRY(hipGetLastError());
     }
     return 0;
   }
@@ -1023,7 +1207,7 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
   if (!pl.direct) {
     CompactArgs c;
     memset(&c, 0, sizeof(c));
-    c.conv = 0; c.words = pl.words; c.L = L; c.times = in->d_times; c.src = in->d_src;
+    c.words = pl.words; c.L = L; c.times = in->d_times;
     c.n_real = in->d_n_real; c.masks = a.masks; c.cap = out->cap;
     c.fill_pads = out->fill_pads; c.out_t = out->d_times; c.out_s = out->d_src;
     c.out_n = out->d_n;
@@ -1108,7 +1292,7 @@ int32_t salt_layer_workspace_size(const salt_layer_desc* desc, const salt_qparam
     ConvPlan pl;
     rc = plan_conv(desc, prm, B, want_neuron_extremes != 0, desc->max_queue_len >= L, &pl);
     if (rc) return rc;
-    *bytes = mask_bytes_conv(pl, desc, B, L);
+    *bytes = mask_bytes_conv(pl, B, L);
   } else {
     FcPlan pl;
     plan_fc(desc, &pl);

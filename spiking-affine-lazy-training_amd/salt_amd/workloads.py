@@ -122,7 +122,9 @@ def config3(B=1024, n_mean=4500, caps=(16384, 16384, 16384)) -> Workload:
 
 
 def config4(B=64, n_events=65536) -> Workload:
-    """conv 2 -> 32, 3x3, s1 on 128x128x2 (126x126x32 registers per stream)."""
+    """conv 2 -> 32, 3x3, s1 on 128x128x2 (126x126x32 registers per stream); the output
+    capacity is the reference's default max_out_spikes (salt_core/layers/conv.py:50), far
+    above the few spikes per stream this input gives."""
     w = _weight_rng(4)
     streams = []
     for r in _children(4, B):
@@ -131,7 +133,7 @@ def config4(B=64, n_events=65536) -> Workload:
         streams.append((t, (p * 128 * 128 + y * 128 + x).astype(np.int32)))
     ev = _pad(streams)
     layer = ConvLayer(name="conv1", ic=2, h_in=128, w_in=128, oc=32, k=3, s=1, p=0, init_k=1.0,
-                      tau=30.0, max_queue_len=n_events + 1, max_out_spikes=1 << 20)
+                      tau=30.0, max_queue_len=n_events + 1, max_out_spikes=8192)
     params = [_params(_codes(w, (32, 2, 3, 3), 24.0, 8), 30.0, 200)]
     return Workload("c4_conv2x32k3_128", Network((2, 128, 128), [layer]), params, ev, "round")
 

@@ -52,9 +52,11 @@ def test_workspace_size_is_host_only(monkeypatch):
     d = _lib.LayerDesc()
     d.kind, d.ic, d.h_in, d.w_in, d.oc, d.k, d.s, d.p = _lib.SALT_LAYER_CONV, 2, 128, 128, 32, 3, 1, 0
     d.max_queue_len, d.max_out_spikes = 100, 16
-    # partitioned (row bands): per-event spike masks, then one spike count per (stream,
-    # 2048-event compaction segment), then (unless turned off) each band's event list
-    masks_and_counts = 64 * 1000 * 32 * 4 + 64 * 1 * 4
+    # partitioned (row bands of >= 2 rows, 5 channel groups of one iteration): a validity
+    # word per event, the spike words of the 2 bands an event reaches at most (one 8-byte
+    # word per channel group), one spike count per (stream, 2048-event compaction
+    # segment), then (unless turned off) each band's event list
+    masks_and_counts = 64 * 1000 * 4 + 64 * 1000 * 2 * 5 * 8 + 64 * 1 * 4
     monkeypatch.setenv("SALT_CONV_BANDLIST", "0")
     rc = _lib.lib().salt_layer_workspace_size(ctypes.byref(d), ctypes.byref(_qp()), 64, 1000, 0,
                                              ctypes.byref(size))

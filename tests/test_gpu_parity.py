@@ -125,6 +125,8 @@ def test_fc_waves_per_stream_match_oracle(waves, monkeypatch):
             geom, prm, ocap = oracle_spec(layer, params, rm)
             ref = O.layer_forward(geom, prm, times, src, n_real, ocap)
             assert int(ref["out_n"].sum()) > 64 * B, "the case must fire densely"
+            if n_out >= 300:  # chunks of more than two spikes per event: the dense placement
+                assert (ref["out_n"] / np.maximum(n_real, 1)).max() > 2
             assert_layer_equal(out, ref, tag=f"waves {waves} {n_out} {cap}")
 
 @pytest.mark.parametrize("spw", [2, 3, 4, 5])
@@ -231,17 +233,19 @@ def test_conv_row_bands_with_and_without_event_lists(lists, monkeypatch):
     """Row-band plans (planes above the LDS size) whose work-groups decode their band's
     event list, or the whole stream (SALT_CONV_BANDLIST=0): same streams, registers and
     extremes as the oracle, for stride 1 and for stride 2 with padding (events meeting
-    two bands), uniform and clustered sources."""
+    two bands), uniform and clustered sources, and streams longer than one segment of
+    the list build (1024 events)."""
     monkeypatch.setenv("SALT_CONV_BANDLIST", lists)
     for mi, (case, clustered) in enumerate([((1, 130, 130, 4, 3, 1, 0, 3, 700), False),
-                                            ((2, 200, 200, 4, 5, 2, 2, 3, 600), True)]):
+                                            ((2, 200, 200, 4, 5, 2, 2, 3, 600), True),
+                                            ((1, 130, 130, 4, 3, 1, 0, 2, 3500), True)]):
         ic, h, w, oc, k, s, p, B, L = case
         rng = np.random.default_rng(1300 + 10 * int(lists) + mi)
         layer = ConvLayer(name="c", ic=ic, h_in=h, w_in=w, oc=oc, k=k, s=s, p=p, init_k=1.0,
                           max_queue_len=int(rng.choice([L + 1, max(2, L // 25)])),
                           max_out_spikes=4 * L * oc)
         params, rm = _params(rng, layer.weight_shape, layer.n_neurons, oc, MODES[mi + 1], 8,
-                             ["channel", "neuron"][mi])
+                             ["channel", "neuron", "scalar"][mi])
         times, src, n_real = _events(rng, B, L, ic * h * w)
         if clustered:
             src = _clustered_sources(rng, B, L, ic, h, w, 3 * k)
