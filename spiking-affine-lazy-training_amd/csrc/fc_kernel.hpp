@@ -193,25 +193,36 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
         // consecutive entries (whole cache lines from one wave in quick succession)
         // instead of one entry in each of 64 runs.  Measured on configuration 5 (~180
         // spikes per event): 63.7 -> 42.0 ms, writes 110 -> 70 GB for 66 GB of entries.
+        // Stores address the uniform stream bases plus a 32-bit byte offset (the
+        // scalar-base form of the store); the capacity test only in the event that
+        // reaches it.
         const int te_bits = __float_as_int(ms_time(tv));
-        for (uint64_t evs = __ballot(cnt > 0); evs; evs &= evs - 1) {
-          const int e = __builtin_ctzll(evs);
-          int at = __builtin_amdgcn_readlane(first, e);
-          if (at >= room) break;  // so do the later events'
+        char* const otb = reinterpret_cast<char*>(ot);
+        char* const osb = reinterpret_cast<char*>(os);
+        const uint64_t lane_bit = 1ull << lane;
+        auto place = [&](int e, int at, auto check) {
+          constexpr bool kCheck = decltype(check)::value;
           const float te = __int_as_float(__builtin_amdgcn_readlane(te_bits, e));
 #pragma unroll
           for (int k = 0; k < NPL; ++k) {
             const uint64_t m =
                 ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(sp[k] >> 32), e) << 32) |
                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)sp[k], e);
-            const int r = at + (int)__builtin_amdgcn_mbcnt_hi(
+            const uint32_t r = (uint32_t)at + __builtin_amdgcn_mbcnt_hi(
                                    (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            if (((m >> lane) & 1ull) && r < room) {
-              ot[r] = te;
-              os[r] = n0 + k * kWave + lane;
+            if ((m & lane_bit) && (!kCheck || (int)r < room)) {
+              *reinterpret_cast<float*>(otb + (r << 2)) = te;
+              *reinterpret_cast<int32_t*>(osb + (r << 2)) = n0 + k * kWave + lane;
             }
             at += __popcll(m);
           }
+        };
+        for (uint64_t evs = __ballot(cnt > 0); evs; evs &= evs - 1) {
+          const int e = __builtin_ctzll(evs);
+          const int at = __builtin_amdgcn_readlane(first, e);
+          if (at >= room) break;  // so do the later events'
+          if (at + __builtin_amdgcn_readlane(cnt, e) <= room) place(e, at, std::false_type{});
+          else place(e, at, std::true_type{});
         }
       } else {
         // Sparse chunk: each lane writes its event's run (a few stores in all).
