@@ -1,6 +1,16 @@
-"""A quantized conv layer as the $readmemh hex text files of the SALT-FPGA conv RTL
-(salt_core/fpga_export.py): packed weight words, per-output-channel thresholds, decay
-table.  One value per line, fixed ceil(width/4) hex digits, zero-padded."""
+"""A quantized conv layer as the $readmemh text files the SALT-FPGA conv RTL loads (the
+files of salt_core/fpga_export.py): one value per line, each a fixed ceil(width/4) hex
+digits, zero-padded.
+
+* <layer>_weight.mem: line oc*C + c holds the K*K taps of that (output, input) channel
+  pair as one word, tap ky*K + kx in bits [tap*b, (tap+1)*b) as b-bit two's complement.
+* <layer>_threshold.mem: one threshold per output channel, (i_V + f_V)-bit two's
+  complement.
+* <layer>_decay.mem: line dt-1 holds the decay code A[dt], f_a-bit unsigned.
+
+Every range and shape check of a layer runs before any of its files is written.  Error
+texts are the reference's.
+"""
 from __future__ import annotations
 
 import os
@@ -11,103 +21,104 @@ import numpy as np
 
 
 def hex_line(value: int, width: int) -> str:
-    """A width-bit unsigned value as ceil(width/4) hex digits (fpga_export.py:15-24)."""
+    """A width-bit unsigned value as ceil(width/4) hex digits."""
     if width < 1:
         raise ValueError(f"位元寬要至少 1,拿到 {width}")
-    if not 0 <= value < (1 << width):
+    if value < 0 or value >> width:
         raise ValueError(f"{value} 超出 {width} 位元無號範圍")
-    return f"{value:0{(width + 3) // 4}x}"
-
-
-def _checked_signed(values, width: int, what: str) -> np.ndarray:
-    if width < 1:
-        raise ValueError(f"{what}的位元寬要至少 1,拿到 {width}")
-    values = np.asarray(values)
-    low, high = -(1 << (width - 1)), (1 << (width - 1)) - 1
-    if values.size and (values.min() < low or values.max() > high):
-        raise ValueError(f"{what} 範圍 {values.min()} ~ {values.max()} 超出 {width} 位元二補數 "
-                         f"{low} ~ {high}")
-    return values.astype(object)
+    return format(value, f"0{-(-width // 4)}x")
 
 
 def twos_complement(value: int, width: int) -> int:
-    """A signed value as its width-bit two's-complement bit pattern."""
-    return int(value) & ((1 << width) - 1)
+    """The width-bit two's-complement pattern of a signed value (range checked by the
+    caller)."""
+    return int(value) % (1 << width)
+
+
+def _as_patterns(values, width: int, what: str) -> list[int]:
+    """Signed values -> their width-bit two's-complement patterns (Python ints, any
+    width); a value outside the signed range, or width < 1, raises ValueError."""
+    if width < 1:
+        raise ValueError(f"{what}的位元寬要至少 1,拿到 {width}")
+    arr = np.asarray(values)
+    lo, hi = -(1 << (width - 1)), (1 << (width - 1)) - 1
+    if arr.size and not (lo <= arr.min() and arr.max() <= hi):
+        raise ValueError(f"{what} 範圍 {arr.min()} ~ {arr.max()} 超出 {width} 位元二補數 "
+                         f"{lo} ~ {hi}")
+    return [twos_complement(v, width) for v in arr.reshape(-1).tolist()]
 
 
 def conv_weight_lines(q, weight_width: int) -> list[str]:
-    """Weight file lines (fpga_export.py:44-64): address oc*C + c holds one K*K*b-bit
-    word, tap ky*K + kx at bit (ky*K + kx)*b.  q must be (OC, C, K, K) within b-bit two's
-    complement."""
+    """The weight file's lines for codes q of shape (OC, C, K, K)."""
     q = np.asarray(q)
     if q.ndim != 4 or q.shape[2] != q.shape[3]:
         raise ValueError(f"q 要是 (OC, C, K, K),拿到形狀 {q.shape}")
-    oc, ic, k, _ = q.shape
-    codes = _checked_signed(q, weight_width, "權重碼").reshape(oc * ic, k * k)
+    taps = q.shape[2] * q.shape[3]
+    patterns = _as_patterns(q, weight_width, "權重碼")
     lines = []
-    for kernel in codes:
+    for start in range(0, len(patterns), taps):
         word = 0
-        for tap, code in enumerate(kernel):
-            word |= twos_complement(code, weight_width) << (tap * weight_width)
-        lines.append(hex_line(word, k * k * weight_width))
+        for p in reversed(patterns[start:start + taps]):  # the last tap is the top field
+            word = (word << weight_width) | p
+        lines.append(hex_line(word, taps * weight_width))
     return lines
 
 
 def channel_thresholds(v_th_int, out_channels: int) -> np.ndarray:
-    """Per-neuron (or scalar) thresholds -> one per output channel; a channel whose
-    neurons disagree raises ValueError (fpga_export.py:67-83)."""
-    v_th_int = np.asarray(v_th_int)
-    if v_th_int.ndim == 0:
-        return np.full(out_channels, v_th_int.item())
-    if v_th_int.ndim != 1 or v_th_int.size % out_channels != 0:
-        raise ValueError(f"v_th_int 形狀 {v_th_int.shape} 不能分成 {out_channels} 個 output channel")
-    per_channel = v_th_int.reshape(out_channels, -1)
-    mismatched = np.flatnonzero((per_channel != per_channel[:, :1]).any(axis=1))
-    if mismatched.size:
-        raise ValueError(f"output channel {mismatched.tolist()} 的門檻不全相同")
-    return per_channel[:, 0]
+    """One threshold per output channel from a scalar or a per-neuron array (neuron
+    oc*H*W + y*W + x); a channel whose neurons disagree raises ValueError."""
+    v = np.asarray(v_th_int)
+    if v.ndim == 0:
+        return np.full(out_channels, v.item())
+    if v.ndim != 1 or v.size % out_channels:
+        raise ValueError(f"v_th_int 形狀 {v.shape} 不能分成 {out_channels} 個 output channel")
+    rows = v.reshape(out_channels, -1)
+    uneven = np.flatnonzero(rows.min(axis=1) != rows.max(axis=1))
+    if uneven.size:
+        raise ValueError(f"output channel {uneven.tolist()} 的門檻不全相同")
+    return rows[:, 0].copy()
 
 
 def threshold_lines(thresholds, membrane_width: int) -> list[str]:
-    """Thresholds as membrane_width-bit two's complement (fpga_export.py:86-92)."""
-    values = _checked_signed(thresholds, membrane_width, "門檻")
-    return [hex_line(twos_complement(v, membrane_width), membrane_width) for v in values]
+    """Per-channel thresholds as membrane_width-bit two's-complement lines."""
+    return [hex_line(p, membrane_width)
+            for p in _as_patterns(thresholds, membrane_width, "門檻")]
 
 
 def decay_lines(decay_table_int, decay_frac_width: int) -> list[str]:
-    """Decay codes, line dt-1 = A[dt], decay_frac_width-bit unsigned (fpga_export.py:95-100)."""
-    return [hex_line(int(v), decay_frac_width) for v in np.asarray(decay_table_int)]
+    """Decay codes as decay_frac_width-bit unsigned lines (line dt-1 = A[dt])."""
+    return [hex_line(int(a), decay_frac_width) for a in np.asarray(decay_table_int).tolist()]
 
 
 def write_mem(path: str | os.PathLike, lines: Sequence[str]) -> None:
-    Path(path).write_text("".join(f"{line}\n" for line in lines), encoding="ascii")
+    """Lines to a text file, each ended by a newline."""
+    with open(path, "w", encoding="ascii", newline="\n") as f:
+        f.writelines(line + "\n" for line in lines)
 
 
 def write_conv_layer_mem(out_dir: str | os.PathLike, layer, params, weight_width: int
                          ) -> dict[str, Path]:
-    """<name>_weight.mem, <name>_threshold.mem (i_V + f_V bits) and <name>_decay.mem (f_a
-    bits) of one conv layer (fpga_export.py:108-138).  Every check runs before any file
-    is written."""
+    """Writes <name>_weight.mem, <name>_threshold.mem and <name>_decay.mem of one conv
+    layer into out_dir (created if needed); returns {"weight" | "threshold" | "decay":
+    path}.  Shape and range problems raise ValueError before anything is written."""
     q = np.asarray(params.q)
-    if q.shape != (layer.oc, layer.ic, layer.k, layer.k):
-        raise ValueError(f"{layer.name} 的 q 形狀 {q.shape},層的幾何是 "
-                         f"{(layer.oc, layer.ic, layer.k, layer.k)}")
+    geometry = (layer.oc, layer.ic, layer.k, layer.k)
+    if q.shape != geometry:
+        raise ValueError(f"{layer.name} 的 q 形狀 {q.shape},層的幾何是 {geometry}")
     if params.v_th_int is None:
         raise ValueError(f"{layer.name} 沒有門檻,conv 層要能 fire")
-    v_th_int = np.asarray(params.v_th_int)
+    v_th = np.asarray(params.v_th_int)
     n_neurons = layer.oc * layer.h_out * layer.w_out
-    if v_th_int.ndim != 0 and v_th_int.shape != (n_neurons,):
-        raise ValueError(f"{layer.name} 的 v_th_int 形狀 {v_th_int.shape},神經元數 {n_neurons}")
-    contents = {
-        "weight": conv_weight_lines(q, weight_width),
-        "threshold": threshold_lines(channel_thresholds(v_th_int, layer.oc),
-                                     params.i_V + params.f_V),
-        "decay": decay_lines(np.asarray(params.decay_table_int), params.f_a),
-    }
-    out_dir = Path(out_dir)
-    out_dir.mkdir(parents=True, exist_ok=True)
-    paths = {}
-    for kind, lines in contents.items():
-        paths[kind] = out_dir / f"{layer.name}_{kind}.mem"
-        write_mem(paths[kind], lines)
-    return paths
+    if v_th.ndim != 0 and v_th.shape != (n_neurons,):
+        raise ValueError(f"{layer.name} 的 v_th_int 形狀 {v_th.shape},神經元數 {n_neurons}")
+    files = {"weight": conv_weight_lines(q, weight_width),
+             "threshold": threshold_lines(channel_thresholds(v_th, layer.oc),
+                                          params.i_V + params.f_V),
+             "decay": decay_lines(params.decay_table_int, params.f_a)}
+    target = Path(out_dir)
+    target.mkdir(parents=True, exist_ok=True)
+    written = {}
+    for kind, lines in files.items():
+        written[kind] = target / f"{layer.name}_{kind}.mem"
+        write_mem(written[kind], lines)
+    return written

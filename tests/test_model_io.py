@@ -152,6 +152,23 @@ def test_loads_a_file_laid_out_by_hand(tmp_path):
     assert model.metadata == {"decoder": "membrane_regression", "batch_size": 8}
 
 
+@pytest.mark.parametrize("v_th, where", [
+    (np.int32(0), "its scalar threshold"),                           # scalar
+    (np.array([40, 40, -3], np.int32), "channel 2"),                 # per channel
+    (np.where(np.arange(48) == 21, 0, 40).astype(np.int32), "channel 1 (neuron 21)")])
+def test_load_quantized_refuses_nonpositive_thresholds_naming_the_channel(tmp_path, v_th, where):
+    """A threshold <= 0 fires on the reference's pad, catch-up and identity columns
+    (salt_core/quant/scan.py:46-51), which this path does not run: the model is refused
+    when loaded, the message naming the layer and the channel (conv1 has 4 x 4 neurons
+    per channel, so neuron 21 is in channel 1)."""
+    params = _quant_params()
+    params[0] = params[0]._replace(v_th_int=v_th)
+    path = tmp_path / "q.npz"
+    save_quantized(path, NETWORK, params, "round", METADATA)  # writing stays possible
+    with pytest.raises(ValueError, match=rf"conv1: v_th_int = -?\d+ <= 0 at {where.replace('(', '[(]').replace(')', '[)]')}"):
+        load_quantized(path)
+
+
 def test_quantized_param_count_mismatch_raises(tmp_path):
     with pytest.raises(ValueError, match="量化參數"):
         save_quantized(tmp_path / "q.npz", NETWORK, _quant_params()[:1], "round", METADATA)
