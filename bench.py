@@ -45,6 +45,7 @@ LDS_SPEC_GBS = N_CU * 128 * CLOCK_GHZ     # 128 B/clk per CU: the figure before 
 VALU_PEAK_GINST = N_CU * 4 * CLOCK_GHZ / 4  # wave64 VALU instructions / ns: 4 SIMDs, 4 clk each
 PROFILES = os.path.join(ROOT, "profiles")
 LDS_PEAK_FILE = os.path.join(PROFILES, "lds_peak.json")
+HBM_COPY_FILE = os.path.join(PROFILES, "hbm_copy.json")
 TRAFFIC_FILE = os.path.join(PROFILES, "hbm_traffic_{workload}.json")
 SQ_FILE = os.path.join(PROFILES, "sq_insts_{workload}.json")
 COPY_BYTES = 1 << 30                      # --copy-calibration: bytes read (and written)
@@ -64,17 +65,32 @@ def _load_json(path):
 
 # ------------------------------------------------------------------ probes
 
-def copy_calibration() -> int:
+def copy_calibration(out_path: str | None = None) -> int:
     """A plain device-to-device copy of COPY_BYTES, three times: the reference launch
-    whose FETCH_SIZE / WRITE_SIZE readings scale the counters of the layer kernels."""
+    whose FETCH_SIZE / WRITE_SIZE readings scale the counters of the layer kernels.  Each
+    copy is timed with HIP events on the copy's stream; the best of the three gives the
+    measured copy bandwidth (bytes read + bytes written per second), reported beside the
+    published 8 TB/s HBM peak (written to out_path when given)."""
     import torch
     torch.cuda.set_device(0)
     src = torch.ones(COPY_BYTES // 4, dtype=torch.int32, device="cuda")
     dst = torch.empty_like(src)
+    ms = []
     for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
         dst.copy_(src)
-    torch.cuda.synchronize()
-    print(json.dumps({"copy_bytes": COPY_BYTES, "launches": 3}), flush=True)
+        e1.record()
+        e1.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    res = {"copy_bytes": COPY_BYTES, "launches": 3, "ms": [round(m, 4) for m in ms],
+           "GB_per_s": round(2 * COPY_BYTES / (min(ms) * 1e-3) / 1e9, 1),
+           "command": "python3 bench.py --copy-calibration"}
+    line = json.dumps(res)
+    print(line, flush=True)
+    if out_path:
+        with open(out_path, "w", encoding="utf-8") as f:
+            f.write(line + "\n")
     return 0
 
 
@@ -344,14 +360,15 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run the reference copy used to scale HBM traffic counters")
     ap.add_argument("--lds-peak", action="store_true", help="only run the LDS bandwidth probe")
-    ap.add_argument("--out", default=None, help="--lds-peak / --digest: file to write")
+    ap.add_argument("--out", default=None,
+                    help="--lds-peak / --copy-calibration / --digest: file to write")
     ap.add_argument("--digest", default=None, metavar="DIR",
                     help="summarise the rocprofv3 counter CSVs under DIR (no GPU)")
     ap.add_argument("--digest-kind", default="sq", choices=("sq", "traffic"))
     ap.add_argument("--digest-command", default="", help="the profiling command, recorded")
     args = ap.parse_args()
     if args.copy_calibration:
-        return copy_calibration()
+        return copy_calibration(args.out)
     if args.lds_peak:
         return lds_peak(args.out)
     if args.digest:
@@ -431,12 +448,15 @@ def main() -> int:
     dom = max(per_layer, key=lambda d: d["ms"])
     sec = dom["ms"] * 1e-3
     lds_prof = _load_json(LDS_PEAK_FILE)
+    hbm_copy = _load_json(HBM_COPY_FILE)
     lds_peak_gbs = lds_prof["peak_GB_per_s"] if lds_prof else LDS_SPEC_GBS
     traffic = _load_json(TRAFFIC_FILE.format(workload=w.name))
     sq = _load_json(SQ_FILE.format(workload=w.name))
     roofs = {
         "hbm": {"achieved": round(dom["hbm_bytes"] / sec / 1e9, 2), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "algorithmic_bytes": dom["hbm_bytes"]},
+                "unit": "GB/s", "algorithmic_bytes": dom["hbm_bytes"],
+                "measured_copy_GB_per_s": (hbm_copy or {}).get("GB_per_s"),
+                "measured_copy_source": "profiles/hbm_copy.json (bench.py --copy-calibration)"},
         "lds": {"achieved": round(dom["lds_bytes"] / sec / 1e9, 2), "peak": round(lds_peak_gbs, 1),
                 "unit": "GB/s", "algorithmic_bytes": dom["lds_bytes"],
                 "peak_source": "profiles/lds_peak.json (bench.py --lds-peak)" if lds_prof

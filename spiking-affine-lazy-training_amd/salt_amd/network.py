@@ -88,18 +88,41 @@ def check_layer_connections(layers: Sequence) -> None:
         _check_connected(prev.output_shape, nxt.input_shape, prev.name, nxt.name)
 
 
+def _chain(layers: Sequence, weights: Sequence, input_stream: EventStream, backend) -> list:
+    """The layers' outputs, enqueued one after the other with no host synchronisation in
+    between, then one check of every layer's spike counts against its capacity.  Only
+    when a stream overflowed a layer's capacity is that layer (and every layer after it)
+    run again with the reference's truncation, which needs the counts on the host."""
+    outputs, stream = [], input_stream
+    for layer, params in zip(layers, weights):
+        out = backend.layer_forward(layer, params, stream, exact_truncation=False)
+        outputs.append(out)
+        stream = out.stream
+    over = torch.stack([(o.diag.spike_count.reshape(-1) > int(layer.max_out_spikes)).any()
+                        for layer, o in zip(layers, outputs)]).cpu().numpy()
+    if not over.any():
+        return outputs
+    first = int(np.flatnonzero(over)[0])
+    stream = outputs[first - 1].stream if first else input_stream
+    for i in range(first, len(layers)):
+        outputs[i] = layers[i].forward(weights[i], stream, backend=backend)
+        stream = outputs[i].stream
+    return outputs
+
+
 def run_network(layers: Sequence, weights: Sequence, input_stream: EventStream, *,
                 backend: QuantBackend | None = None, trace: bool = False) -> NetworkOutput:
     """Chain layers, each output stream feeding the next (salt_core/network.py:93-122).
     trace: also collect every layer's step-by-step trajectories (LayerForwardTrace)."""
     backend = resolve_backend(backend)
     check_layer_connections(layers)
-    stream = input_stream
-    outputs = []
-    for layer, params in zip(layers, weights):
-        out = layer.forward(params, stream, backend=backend, trace=trace)
-        outputs.append(out)
-        stream = out.stream
+    outputs = _chain(layers, weights, input_stream, backend) if not trace else []
+    if trace:
+        stream = input_stream
+        for layer, params in zip(layers, weights):
+            out = layer.forward(params, stream, backend=backend, trace=True)
+            outputs.append(out)
+            stream = out.stream
     fits = None
     for layer, out in zip(layers, outputs):
         if layer.capacity is not None:

@@ -279,10 +279,15 @@ class QuantBackend:
         return dp
 
     def layer_forward(self, layer, params: QuantizedLayerParams, in_stream: EventStream, *,
-                      fill_pads: bool = True) -> LayerOutput:
+                      fill_pads: bool = True, exact_truncation: bool = True) -> LayerOutput:
         """One layer over a (batched) EventStream on the GPU: the work of
         ConvLayer.forward / FCLayer.forward (salt_core/layers/conv.py:124-149,
-        salt_core/layers/fc.py:84-101) under this backend."""
+        salt_core/layers/fc.py:84-101) under this backend.
+
+        exact_truncation=False: no host synchronisation; a stream with more spikes than
+        the layer's capacity keeps its first cap spikes in event order, not the
+        reference's choice (the first cap in (neuron, column) order) -- for callers that
+        check the counts afterwards and redo such a layer (run_network does)."""
         round_mode = RoundMode(self.round_mode)
         single = in_stream.event_times.dim() == 1
         times = _batched(in_stream.event_times).to(torch.float32).contiguous()
@@ -294,9 +299,9 @@ class QuantBackend:
         cap = int(layer.max_out_spikes)
         raw = run_layer_kernel(layer, dp, round_mode, times, src, n_real, cap,
                                extremes=self.neuron_extremes, fill_pads=fill_pads)
-        n_host = raw.n.cpu().numpy()
         out_t, out_s = raw.times, raw.src
-        if (n_host > cap).any():
+        n_host = raw.n.cpu().numpy() if exact_truncation else None
+        if exact_truncation and (n_host > cap).any():
             # Rerun with room for every spike, then cut as the reference does.
             full = run_layer_kernel(layer, dp, round_mode, times, src, n_real, int(n_host.max()),
                                     extremes=False, fill_pads=False)

@@ -162,3 +162,32 @@ def test_network_over_capacity_feeds_the_capped_stream():
     assert int(one[0].n.max()) > 64
     _same(one, per_layer, "over capacity")
     assert not runner.check_fits(one).all()
+
+
+@pytest.mark.parametrize("caps, overflows", [((64, 8192, 8192), True), ((32768, 32768, 65536), False)])
+def test_run_network_checks_capacities_once_and_redoes_an_overflowing_layer(caps, overflows):
+    """run_network (behind Network.apply_batched) enqueues every layer without a host
+    synchronisation and checks the spike counts once at the end; when a stream overflowed
+    a layer's capacity, that layer and every later one are run again with the reference's
+    truncation.  Either way the result equals chaining layer.forward, which truncates
+    each layer exactly before the next reads it."""
+    from salt_amd.network import run_network
+    from salt_amd.quant.backend import QuantBackend
+    rng = np.random.default_rng(9)
+    net, params = _net(rng, f_a=10, f_V=0, i_V=24, overflow="wrap", vth=_scalar(40),
+                       fc_vth=np.int32(60), caps=caps)
+    stream = _device_stream(net, _events(17, B=8, n_mean=800))
+    be = QuantBackend("round")
+    got = run_network(net.layers, params, stream, backend=be)
+    want, s = [], stream
+    for layer, p in zip(net.layers, params):
+        out = layer.forward(p, s, backend=be)
+        want.append(out)
+        s = out.stream
+    counts = [o.diag.spike_count for o in want]
+    assert bool((counts[0] > caps[0]).any()) == overflows
+    for i, (r, o) in enumerate(zip(got.results, want)):
+        assert bool((r.spike_count == o.result.spike_count).all()), f"layer {i} counts"
+        for f in ("v_final", "v_unfitted_min", "v_unfitted_max", "stream_stats"):
+            assert bool((getattr(r, f) == getattr(o.result, f)).all()), f"layer {i} {f}"
+    assert bool(got.fits.all()) == (not overflows)
