@@ -46,7 +46,7 @@ struct FcArgs {
 // The events of one chunk (one per lane of tv/sv, ne of them) with their decay codes
 // Aj.  DIRECT: the slice is the whole layer and appends spikes to the output stream;
 // otherwise it writes the chunk's spike-mask words.
-template <typename QT, int NPL, bool F24, bool SAT, bool WLDS, bool DIRECT>
+template <typename QT, int NPL, bool F24, bool SAT, bool WLDS, bool NOFIRE, bool DIRECT>
 __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const QT* qt,
                                           const int (&col)[NPL], int sw, int n0, int b,
                                           int base, int ne, int tv, int sv, int Aj,
@@ -99,10 +99,14 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
       const uint32_t qw = FV0 ? (uint32_t)(int32_t)qc[k] : ((uint32_t)(int32_t)qc[k] << fV);
       const int32_t u = (int32_t)((uint32_t)d + qw);
       const int32_t f = fit_bits<SAT>(u, qz);
-      const bool keep = f < vth[k];
-      V[k] = keep ? f : 0;
       mn[k] = min(mn[k], u);
       mx[k] = max(mx[k], u);
+      if (NOFIRE) {  // no threshold: the write-back is the register's whole chain
+        V[k] = f;
+        if (DIRECT) continue;
+      }
+      const bool keep = NOFIRE || f < vth[k];
+      if (!NOFIRE) V[k] = keep ? f : 0;
       const uint64_t bal = __ballot(keep);
       if (DIRECT) {
         if (LO) stage_to_lane_lo(klo[k], bal, e);
@@ -153,7 +157,7 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
     if (lo) run(std::true_type{}, std::false_type{});
     else run(std::false_type{}, std::false_type{});
   }
-  if (DIRECT) {
+  if (DIRECT && !NOFIRE) {
     // Lane = the chunk's event: its spikes (neurons ascending) follow those of the
     // chunk's earlier events -- the (event, neuron) order of salt_core/stream.py.
     uint64_t sp[NPL];
@@ -246,7 +250,9 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
   }
 }
 
-template <typename QT, int NPL, bool F24, bool SAT, bool WLDS>
+// NOFIRE: the layer has no threshold (v_th None: a readout), so nothing fires, no spike
+// is staged or placed, and the register's chain per event ends at the write-back.
+template <typename QT, int NPL, bool F24, bool SAT, bool WLDS, bool NOFIRE = false>
 __global__ void __launch_bounds__(kFcMaxWaves * kWave) fc_layer_kernel(FcArgs a) {
   extern __shared__ int32_t dyn[];
   const int lane = threadIdx.x & (kWave - 1);
@@ -318,10 +324,12 @@ __global__ void __launch_bounds__(kFcMaxWaves * kWave) fc_layer_kernel(FcArgs a)
     const int Aj = ext[decay_slot(tv - tp, ntab)];
     t_prev = rdlane(tv, ne - 1);
     if (a.direct)
-      fc_events<QT, NPL, F24, SAT, WLDS, true>(a, wl, qt, col, sw, n0, b, base, ne, tv, sv, Aj,
+      fc_events<QT, NPL, F24, SAT, WLDS, NOFIRE, true>(a, wl, qt, col, sw, n0, b, base, ne, tv,
+                                                       sv, Aj,
                                                V, mn, mx, vth, out_base, merge);
     else
-      fc_events<QT, NPL, F24, SAT, WLDS, false>(a, wl, qt, col, sw, n0, b, base, ne, tv, sv,
+      fc_events<QT, NPL, F24, SAT, WLDS, NOFIRE, false>(a, wl, qt, col, sw, n0, b, base, ne, tv,
+                                                        sv,
                                                 Aj, V, mn, mx, vth, out_base, merge);
   }
   // Pad columns (j >= n_real) are identity with code 0 (connectivity/fc.py:32, :60-61):

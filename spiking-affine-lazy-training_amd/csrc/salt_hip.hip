@@ -1197,7 +1197,8 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
   a.stats = res->d_stats;
   a.masks = static_cast<uint32_t*>(d_workspace);
   if (!pl.direct && (rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
-  const int flags = (f24 ? kFcF24 : 0) | (sat ? kFcSat : 0) | (wlds ? kFcWlds : 0);
+  const int flags = (f24 ? kFcF24 : 0) | (sat ? kFcSat : 0) | (wlds ? kFcWlds : 0) |
+                    (prm->v_th_kind == SALT_VTH_NONE ? kFcNoFire : 0);
   const dim3 grid(pl.n_slices, B);
   switch (prm->q_bits) {
     case 8: HIP_TRY(launch_fc_q8(a, pl.npl, flags, grid, pl.wpg, lds, st)); break;
