@@ -125,6 +125,31 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
   // scheduling barriers keep each load where it is written: left alone, the compiler
   // sinks a load past the preceding event's arithmetic to just before its own use, and
   // the event then waits for the whole LDS latency.
+  if constexpr (DIRECT && NOFIRE && NPL == 1) {
+    if (ne == kWave) {
+      // A full chunk of a readout (one word of neurons, nothing fires): the weights of
+      // all 64 events are loaded first, then the 64 updates run unrolled, so the wave
+      // waits only on the register's own chain.
+      int32_t qv[kWave];
+#pragma unroll
+      for (int i = 0; i < kWave; ++i) {
+        if (WLDS) qv[i] = (int32_t)wl[rdlane(rowv, i) + col[0]];
+        else qv[i] = (int32_t)qt[(size_t)rdlane(sv, i) * a.n_out + n0 + col[0]];
+      }
+      // (folding the weight into a 64-bit multiply-add shortens the chain -- 27 against
+      // 38 clock ticks per update in isolation on gfx950 -- but left this kernel's time
+      // unchanged, 0.140-0.143 ms for configuration 3's readout)
+#pragma unroll
+      for (int i = 0; i < kWave; ++i) {
+        const int32_t d = decay_mul<F24>(V[0], rdlane(Aj, i), fa, rc);
+        const int32_t u = (int32_t)((uint32_t)d + ((uint32_t)qv[i] << fV));
+        V[0] = fit_bits<SAT>(u, qz);
+        mn[0] = min(mn[0], u);
+        mx[0] = max(mx[0], u);
+      }
+      return;
+    }
+  }
   QT q0[NPL], q1[NPL], q2[NPL];
   int A0 = 0, A1 = 0, A2 = 0;
   load(q0, A0, 0);
