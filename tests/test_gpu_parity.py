@@ -105,6 +105,31 @@ def test_fc_matches_oracle(case, mi):
 
 
 
+@pytest.mark.parametrize("bits", [8, 16, 32])
+def test_fc_readouts_without_threshold_match_oracle(bits):
+    """FC layers with no threshold (v_th None, the readout variant: full chunks of 64
+    events unrolled, weights loaded first): weights of every width, from LDS (a small
+    slice) and from global memory (a wide one, or two waves per stream), streams that
+    end on a chunk boundary, inside one and that are empty, wrap and saturate with
+    values pushed past the register range."""
+    for mi, (n_in, n_out, B, L) in enumerate([(300, 10, 5, 64 * 5), (2312, 64, 3, 64 * 3 + 17),
+                                              (37, 128, 4, 150), (1568, 10, 4, 64 * 2 + 1)]):
+        rng = np.random.default_rng(5100 + 10 * bits + mi)
+        layer = FCLayer(name="f", n_in=n_in, n_out=n_out, init_k=1.0, max_out_spikes=16)
+        mode = MODES[(mi + bits // 8) % len(MODES)]
+        params, rm = _params(rng, layer.weight_shape, n_out, n_out, mode, bits, "none")
+        times, src, n_real = _events(rng, B, L, n_in)
+        n_real[0], n_real[-1] = L, 0
+        if B > 2:
+            n_real[1] = 64
+        print("fc readout", bits, (n_in, n_out, B, L), mode, flush=True)
+        out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+        geom, prm, cap = oracle_spec(layer, params, rm)
+        ref = O.layer_forward(geom, prm, times, src, n_real, cap)
+        assert int(ref["out_n"].max()) == 0
+        assert_layer_equal(out, ref, tag=f"readout {bits} {n_out}")
+
+
 @pytest.mark.parametrize("waves", ["1", "2", "4"])
 def test_fc_waves_per_stream_match_oracle(waves, monkeypatch):
     """Dense firing (thresholds of a few units) with the neurons of a stream on 1, 2 or 4
