@@ -119,17 +119,13 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
       }
     }
   };
-  // Three events per iteration with three operand sets, each loaded two events before
-  // its use: the loads' latency is covered by two events of arithmetic and no register
-  // has to be copied or widened before its use (either would wait for the load).  The
-  // scheduling barriers keep each load where it is written: left alone, the compiler
-  // sinks a load past the preceding event's arithmetic to just before its own use, and
-  // the event then waits for the whole LDS latency.
+  // A full chunk of a readout (no threshold, a slice of one word of neurons appending
+  // directly): the weights of all 64 events are loaded first, then the 64 updates run
+  // unrolled, so the wave waits only on the register's own chain (configuration 3's
+  // readout 0.181 -> 0.142 ms).  The same for slices that fire, with the ballots staged
+  // at immediate lane indices, measured slower (configuration 1: 0.30 -> 0.33 ms).
   if constexpr (DIRECT && NOFIRE && NPL == 1) {
     if (ne == kWave) {
-      // A full chunk of a readout (one word of neurons, nothing fires): the weights of
-      // all 64 events are loaded first, then the 64 updates run unrolled, so the wave
-      // waits only on the register's own chain.
       int32_t qv[kWave];
 #pragma unroll
       for (int i = 0; i < kWave; ++i) {
@@ -138,7 +134,7 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
       }
       // (folding the weight into a 64-bit multiply-add shortens the chain -- 27 against
       // 38 clock ticks per update in isolation on gfx950 -- but left this kernel's time
-      // unchanged, 0.140-0.143 ms for configuration 3's readout)
+      // unchanged, 0.140-0.143 ms)
 #pragma unroll
       for (int i = 0; i < kWave; ++i) {
         const int32_t d = decay_mul<F24>(V[0], rdlane(Aj, i), fa, rc);
@@ -150,6 +146,12 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
       return;
     }
   }
+  // Three events per iteration with three operand sets, each loaded two events before
+  // its use: the loads' latency is covered by two events of arithmetic and no register
+  // has to be copied or widened before its use (either would wait for the load).  The
+  // scheduling barriers keep each load where it is written: left alone, the compiler
+  // sinks a load past the preceding event's arithmetic to just before its own use, and
+  // the event then waits for the whole LDS latency.
   QT q0[NPL], q1[NPL], q2[NPL];
   int A0 = 0, A1 = 0, A2 = 0;
   load(q0, A0, 0);
