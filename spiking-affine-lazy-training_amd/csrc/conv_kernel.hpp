@@ -2,9 +2,12 @@
 // salt_core/connectivity/conv.py and the scan of salt_core/quant/scan.py:22-132).
 //
 // A work-group owns one stream and a band of R output rows (in-kernel output: the whole
-// plane).  Its waves split that band into ncg channel groups x nsb sub-bands of Rw rows;
-// each wave processes, in order, the stream's events whose candidate rows meet its
-// sub-band, as decoded by the sub-band's first channel group.  Everything a wave touches
+// plane).  Its channel-group waves split that band into ncg channel groups x nsb
+// sub-bands of Rw rows; each processes, in order, the stream's events whose candidate
+// rows meet its sub-band, as decoded by the sub-band's helper wave, which also places
+// the sub-band's spikes in the output (so a channel group's wave runs nothing but its
+// events: the decode and the placement take a quarter of a stream's time when the
+// channel groups do them themselves, measured on one stream).  Everything a wave touches
 // per event lives in LDS: registers V[channel slot][position], per-position (last-update
 // time, queue count), and -- shared -- the weight codes of its channel group and the
 // extended decay table.
@@ -18,7 +21,7 @@
 //   weight    = (c*K*K + (y+P-oy0*S)*K + (x+P-ox0*S)) + [slot*QS - dy*S*K - dx*S]
 // where Wp >= W is the row stride of the position arrays in LDS and VS, QS the slot
 // strides, chosen on the host so that a wave's accesses spread over the LDS banks
-// (the padding columns are never touched).  The decoding wave turns 64 events at a time
+// (the padding columns are never touched).  The helper wave turns 64 events at a time
 // (one per lane) into LDS records: those two bases, the time and a 64-bit mask of the
 // candidates in the output plane and its sub-band; the loop reads one record per event
 // (a broadcast).
@@ -29,29 +32,35 @@
 // code give U = 0 and never fire, and the extremes start at 0.  Channel slots past a
 // wave's channels likewise hold zero codes and an unreachable threshold.
 //
-// Output.  With the whole plane in the work-group, each wave stores the ballot of its
-// spikes per (chunk event, iteration) and its spike count per chunk event in LDS; after
-// the chunk's barrier every wave places its own spikes in the stream's output, in the
-// order (event, channel group, iteration, lane) = (event, ascending neuron id) of
-// salt_core/stream.py:24-46, from a scan of all the stream's waves' counts.  With
+// Output.  With the whole plane in the work-group, each channel-group wave stores the
+// ballot of its spikes per (chunk event, iteration) and its spike count per chunk event
+// in LDS; in the next chunk the helper wave places every group's spikes in the stream's
+// output, in the order (event, channel group, iteration, lane) = (event, ascending neuron
+// id) of salt_core/stream.py:24-46, from a scan of all the stream's waves' counts.  With
 // several work-groups per stream (state above the LDS size: bands of rows) the waves
-// stage the same ballots; after the chunk's barrier, for each event with a spike in the
-// band, every wave stores its ballots as 64-bit spike words in global memory, in the
+// stage the same ballots; in the next chunk, for each event with a spike in the band, the
+// helper stores every group's ballots as 64-bit spike words in global memory, in the
 // event's slot for this band, and marks the slot valid; a compaction kernel orders them.
 // Nothing is stored for an event without a spike in the band, and only the validity
 // words need clearing before the launch.
 //
 // One barrier per 64-event chunk, none inside the event loop: a wave's LDS operations
-// complete in program order, so event e+1 reads what event e wrote.  The decoding wave
-// decodes the next chunk while the others start this one (double-buffered records).
+// complete in program order, so event e+1 reads what event e wrote.  The helper decodes
+// the next chunk and places the previous one's spikes while the channel groups run this
+// one (double-buffered records and ballots).
 #pragma once
 
 #include "salt_device.hpp"
 
 namespace salt {
 
-constexpr int kConvMaxWaves = 8;     // waves per stream (channel groups x sub-bands)
+constexpr int kConvMaxWaves = 8;     // channel-group waves per stream (groups x sub-bands)
 constexpr int kConvBlockWaves = 16;  // waves per work-group (streams x waves per stream)
+
+// Waves of a work-group: per stream, its channel-group waves and one helper per sub-band.
+__host__ __device__ inline int conv_block_waves(int spw, int ncg, int nsb) {
+  return spw * (ncg * nsb + nsb);
+}
 
 // Geometry of a conv layer as the device code uses it.
 struct ConvGeom {
@@ -634,9 +643,15 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int lane = tid & (kWave - 1);
   const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int nthr = blockDim.x;
-  // Wave wv serves stream slot ks of the work-group's spw streams, as its wave wl.
+  // Waves [0, spw * nwps): wave wv serves stream slot ks of the work-group's spw streams,
+  // as its channel-group wave wl.  Then one helper wave per (stream slot, sub-band), which
+  // decodes the events and places every channel group's spikes.
   const int nwps = a.ncg * a.nsb;
-  const int ks = wv / nwps, wl = wv - ks * nwps;
+  const int nch = a.spw * nwps;
+  const bool helper = wv >= nch;
+  const int hw = wv - nch;
+  const int ks = helper ? hw / a.nsb : wv / nwps;
+  const int wl = helper ? 0 : wv - ks * nwps;
   // Row-band plans: the bands of a stream read the same events, so they run on one XCD.
   const int n_wg = gridDim.x * gridDim.y;
   const int lin = blockIdx.y * gridDim.x + blockIdx.x;
@@ -644,7 +659,8 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int bx = wg % gridDim.x, by = wg / gridDim.x;  // (band, group of streams)
   const int b = by * a.spw + ks;
   const bool live = b < a.B;  // the last work-group's slots past the batch have no stream
-  const int cg = wl % a.ncg, sb = wl / a.ncg;  // channel group, sub-band
+  const int cg = wl % a.ncg;                        // channel group (helper: none, 0)
+  const int sb = helper ? hw - ks * a.nsb : wl / a.ncg;  // sub-band
   const int Gi = a.Gi, Gp = NIT * a.Gi;
   const int oc0 = cg * a.G;
   const int ocn = max(0, min(a.G, g.OC - oc0));
@@ -659,8 +675,8 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
                                       PWs, npos, EXT, VTHN, NOTRUNC, PAIR);
   const int VS = lay.vs, QS = lay.qst;
   constexpr int RS = PAIR ? 2 : 1;  // records per step
-  // regions: this (stream, sub-band)'s, the stream's sub-band 0's, this wave's, and the
-  // stream's first wave's
+  // regions: this (stream, sub-band)'s, the stream's sub-band 0's, this wave's (none for a
+  // helper wave: it touches no per-wave array), and the stream's first wave's
   int32_t* const band = smem + lay.shared_words + (ks * a.nsb + sb) * lay.band_words;
   int32_t* const band0 = smem + lay.shared_words + ks * a.nsb * lay.band_words;
   int32_t* const wbase = smem + lay.waves + wv * lay.wave_words;
@@ -676,10 +692,9 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   ConvLane c;
   c.ext = ext;
   c.qs = smem + lay.qs + cg * Gp * QS;
-  // The first channel group of a (stream, sub-band) decodes its events (and, NOTRUNC,
-  // keeps the queue counts); the other channel groups see the same events and read its
-  // records.
-  const bool dec = cg == 0;
+  // The helper wave of a (stream, sub-band) decodes its events (and, NOTRUNC, keeps the
+  // queue counts); the channel groups read its records.
+  const bool dec = helper;
   c.tc = reinterpret_cast<int2*>(wbase + lay.tc);
   c.cnt = band + lay.cnt;
   int32_t* const cnt_kept = (NOTRUNC && dec) ? c.cnt : nullptr;
@@ -706,26 +721,27 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
                            : 0;
   }
   // ---- this wave's state
-  for (int i = lane; i < Gp; i += kWave) {
-    int v = INT_MAX;  // unreachable: registers stay below 2^29
-    if (i < ocn) {
-      if (qz.vth_kind == SALT_VTH_SCALAR) v = qz.vth_scalar;
-      else if (qz.vth_kind == SALT_VTH_PER_CHANNEL) v = qz.vth[oc0 + i];
+  if (!helper) {
+    for (int i = lane; i < Gp; i += kWave) {
+      int v = INT_MAX;  // unreachable: registers stay below 2^29
+      if (i < ocn) {
+        if (qz.vth_kind == SALT_VTH_SCALAR) v = qz.vth_scalar;
+        else if (qz.vth_kind == SALT_VTH_PER_CHANNEL) v = qz.vth[oc0 + i];
+      }
+      vthc[i] = v;
     }
-    vthc[i] = v;
-  }
-  for (int i = lane; i < Gp * VS; i += kWave) {
-    c.Vs[i] = 0;
-    if (EXT) { c.mn[i] = 0; c.mx[i] = 0; }
-    if (VTHN) {
-      const int s = i / VS, p = i - s * VS, row = p / Wp, col = p - row * Wp;
-      c.th[i] = (s < ocn && row < rn && col < W)
-                    ? qz.vth[(size_t)(oc0 + s) * g.HW + (r0 + row) * W + col]
-                    : INT_MAX;
+    for (int i = lane; i < Gp * VS; i += kWave) {
+      c.Vs[i] = 0;
+      if (EXT) { c.mn[i] = 0; c.mx[i] = 0; }
+      if (VTHN) {
+        const int s = i / VS, p = i - s * VS, row = p / Wp, col = p - row * Wp;
+        c.th[i] = (s < ocn && row < rn && col < W)
+                      ? qz.vth[(size_t)(oc0 + s) * g.HW + (r0 + row) * W + col]
+                      : INT_MAX;
+      }
     }
-  }
-  for (int i = lane; i < (NOTRUNC ? 1 : 2) * lay.tcn; i += kWave) wbase[lay.tc + i] = 0;
-  if (dec) {
+    for (int i = lane; i < (NOTRUNC ? 1 : 2) * lay.tcn; i += kWave) wbase[lay.tc + i] = 0;
+  } else {
     if (NOTRUNC)
       for (int i = lane; i < PWs; i += kWave) c.cnt[i] = 0;
     if (lane < 2 * RS)  // the records after a full chunk: no candidate
@@ -823,9 +839,9 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
       evt0[(k % kConvEvtBufs) * kWave + lane] =
           a.merge ? make_int2(tv, oy0 * W + ox0) : make_int2(j, 0);
   };
-  // Row bands, every wave: for each event of chunk k with a spike in the band, its own
-  // spike words (all NIT, spikes or not) in the event's slot for this band; the first
-  // channel group marks the slot valid and adds the event's spikes in the band to its
+  // Row bands, the helper wave: for each event of chunk k with a spike in the band, every
+  // channel group's spike words (all NIT, spikes or not) in the event's slot for this
+  // band; it marks the slot valid and adds the event's spikes in the band to its
   // compaction segment.  Lane = the event's index in the chunk.
   const int slot = bx % max(a.nslots, 1);
   auto store_words = [&](int k) {
@@ -836,97 +852,105 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     if (tot == 0) return;
     const int jj = evt0[(k % kConvEvtBufs) * kWave + lane].x;
     const size_t ev = (size_t)b * L + jj;
-    uint64_t* const w = a.words + (ev * a.nslots + slot) * (size_t)(a.ncg * NIT) + cg * NIT;
-    const uint64_t* const kept =
-        reinterpret_cast<const uint64_t*>(wbase + lay.stg) + bf * kWave * NIT + lane * NIT;
+    uint64_t* const w = a.words + (ev * a.nslots + slot) * (size_t)(a.ncg * NIT);
+    for (int g2 = 0; g2 < a.ncg; ++g2) {
+      const uint64_t* const kept = reinterpret_cast<const uint64_t*>(
+          swave0 + g2 * lay.wave_words + lay.stg) + bf * kWave * NIT + lane * NIT;
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) w[it] = ~kept[it];
-    if (cg == 0) {
-      atomicOr(&a.valid[ev], 1u << slot);
-      atomicAdd(&a.seg_cnt[(size_t)b * a.nseg + jj / kCompactSeg], tot);
+      for (int it = 0; it < NIT; ++it) w[g2 * NIT + it] = ~kept[it];
     }
+    atomicOr(&a.valid[ev], 1u << slot);
+    atomicAdd(&a.seg_cnt[(size_t)b * a.nseg + jj / kCompactSeg], tot);
   };
-  // Merge mode, every wave: its own spikes of chunk k, at their places in the stream's
-  // output, ordered (event, channel group, iteration, bit) = (event, ascending neuron id)
-  // -- the order of salt_core/stream.py:24-46.  Lane = the event's index in the chunk.
-  // An event's spikes start after those of the chunk's earlier events (a scan of the
-  // stream's waves' counts) and, within it, after the lower channel groups' spikes and
-  // this group's lower iterations and bits; the sub-bands' ballots of one channel group
-  // are disjoint and share the lane mapping, so the bits below a spike are counted in
-  // their union.
+  // Merge mode, the helper wave of each sub-band: the sub-band's spikes of chunk k, at
+  // their places in the stream's output, ordered (event, channel group, iteration, bit) =
+  // (event, ascending neuron id) -- the order of salt_core/stream.py:24-46.  Lane = the
+  // event's index in the chunk.  An event's spikes start after those of the chunk's
+  // earlier events (a scan of the stream's waves' counts) and, within it, after the lower
+  // channel groups' spikes and the group's lower iterations and bits; the sub-bands'
+  // ballots of one channel group are disjoint and share the lane mapping, so the bits
+  // below a spike are counted in their union.
   auto walk = [&](int k) {
     const int bf = k & 1;
-    int tot = 0, before = 0;
-    for (int s2 = 0; s2 < a.nsb; ++s2)  // wave s2 * ncg + g2: sub-band s2, channel group g2
-      for (int g2 = 0; g2 < a.ncg; ++g2) {
-        const int cw = swave0[(s2 * a.ncg + g2) * lay.wave_words + lay.wcnt + bf * kWave + lane];
-        tot += cw;
-        before += g2 < cg ? cw : 0;
-      }
+    auto count = [&](int s2, int g2) {  // wave s2 * ncg + g2: sub-band s2, channel group g2
+      return swave0[(s2 * a.ncg + g2) * lay.wave_words + lay.wcnt + bf * kWave + lane];
+    };
+    int tot = 0;
+    for (int s2 = 0; s2 < a.nsb; ++s2)
+      for (int g2 = 0; g2 < a.ncg; ++g2) tot += count(s2, g2);
     if (__ballot(tot != 0) == 0) return;  // no spike in the chunk
     const int incl = wave_incl_scan(tot);
     const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
     const int2 ev = evt0[(k % kConvEvtBufs) * kWave + lane];  // read with every lane active
     const float te = ms_time(ev.x);
-    int pos = out_base + (incl - tot) + before;
-    const uint64_t* const stg_cg = reinterpret_cast<const uint64_t*>(
-        swave0 + cg * lay.wave_words + lay.stg) + bf * kWave * NIT + lane * NIT;
+    int pos = out_base + (incl - tot);
+    for (int g2 = 0; g2 < a.ncg; ++g2) {
+      const uint64_t* const stg_cg = reinterpret_cast<const uint64_t*>(
+          swave0 + g2 * lay.wave_words + lay.stg) + bf * kWave * NIT + lane * NIT;
+      const int oc0g = g2 * a.G;
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      uint64_t all = 0, mine = 0;
-      for (int s2 = 0; s2 < a.nsb; ++s2) {
-        const uint64_t v = ~stg_cg[s2 * a.ncg * (lay.wave_words / 2) + it];
-        all |= v;
-        mine = s2 == sb ? v : mine;
-      }
-      while (mine) {
-        const int kb = __builtin_ctzll(mine);
-        mine &= mine - 1;
-        const int p = pos + __popcll(all & ((1ull << kb) - 1));
-        const int2 lmk = lanemap[kb];
-        const int oc = oc0 + it * Gi + lmk.x;
-        if (p < a.cap) {
-          a.out_t[(size_t)b * a.cap + p] = te;
-          a.out_s[(size_t)b * a.cap + p] = oc * g.HW + ev.y + lmk.y;
+      for (int it = 0; it < NIT; ++it) {
+        uint64_t all = 0, mine = 0;
+        for (int s2 = 0; s2 < a.nsb; ++s2) {
+          const uint64_t v = ~stg_cg[s2 * a.ncg * (lay.wave_words / 2) + it];
+          all |= v;
+          mine = s2 == sb ? v : mine;
         }
+        while (mine) {
+          const int kb = __builtin_ctzll(mine);
+          mine &= mine - 1;
+          const int p = pos + __popcll(all & ((1ull << kb) - 1));
+          const int2 lmk = lanemap[kb];
+          const int oc = oc0g + it * Gi + lmk.x;
+          if (p < a.cap) {
+            a.out_t[(size_t)b * a.cap + p] = te;
+            a.out_s[(size_t)b * a.cap + p] = oc * g.HW + ev.y + lmk.y;
+          }
+        }
+        pos += __popcll(all);
       }
-      pos += __popcll(all);
     }
     out_base += total;
   };
 
   if (dec && nchunks > 0) decode(0);
   __syncthreads();
+  if (!helper) {
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) vtc[it] = vthc[min(it * Gi + c.oc_lane - oc0, Gp - 1)];
+    for (int it = 0; it < NIT; ++it) vtc[it] = vthc[min(it * Gi + c.oc_lane - oc0, Gp - 1)];
+  }
   // One barrier per chunk: chunk k's records and counts were written before the last
   // barrier; the next chunk's decode writes the other record buffer, whose readers
   // finished before it; the walk of chunk k-1 reads the ballots and counts written
-  // before it, and event info decoded two chunks before the next decode's.
+  // before it (the channel groups write chunk k's into the other buffers meanwhile), and
+  // event info decoded two chunks before the next decode's.
   for (int k = 0; k < nchunks; ++k) {
     const int bf = k & 1;
-    if (dec && k + 1 < nchunks) decode(k + 1);
-    if (k > 0) {
-      if (a.merge) walk(k - 1);
-      else if (live) store_words(k - 1);
+    if (helper) {
+      if (k + 1 < nchunks) decode(k + 1);
+      if (k > 0) {
+        if (a.merge) walk(k - 1);
+        else if (live) store_words(k - 1);
+      }
+    } else {
+      c.rec = recs + bf * conv_recs(PAIR);
+      c.rec1 = recs1 + bf * conv_recs(PAIR);
+      const int n_ev = __builtin_amdgcn_readfirstlane(nev[bf]);
+      c.stg = stgs + bf * kWave * NIT;
+      c.wcnt = wbase + lay.wcnt + bf * kWave;
+      conv_events<NIT, SAT, EXT, VTHN, M32, NOTRUNC, PAIR>(qz, c, vtc, n_ev, k * kWave,
+                                                           vmin_l, vmax_l);
     }
-    c.rec = recs + bf * conv_recs(PAIR);
-    c.rec1 = recs1 + bf * conv_recs(PAIR);
-    const int n_ev = __builtin_amdgcn_readfirstlane(nev[bf]);
-    c.stg = stgs + bf * kWave * NIT;
-    c.wcnt = wbase + lay.wcnt + bf * kWave;
-    conv_events<NIT, SAT, EXT, VTHN, M32, NOTRUNC, PAIR>(qz, c, vtc, n_ev, k * kWave, vmin_l,
-                                                         vmax_l);
     __syncthreads();
   }
-  if (nchunks > 0) {
+  if (helper && nchunks > 0) {
     if (a.merge) walk(nchunks - 1);
     else if (live) store_words(nchunks - 1);
   }
 
   const int T = n_eff > 0 ? time_ms(tb[n_eff - 1]) : 0;
   int maxcnt = 0;
-  if (live)
+  if (live && !helper)
     maxcnt = conv_finish<EXT, NOTRUNC>(qz, c, lane, T, ocn, PW, W, Wp, VS,
                                    (size_t)b * (g.OC * g.HW) + (size_t)oc0 * g.HW + r0 * W,
                                    g.HW, a.v_final, a.v_min, a.v_max, vmin_l, vmax_l);
@@ -938,8 +962,21 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     red[wv * 4 + 2] = maxcnt;
   }
   __syncthreads();
-  if (wl != 0 || !live) return;
-  for (int w = wv + 1; w < wv + nwps; ++w) {  // the stream's other waves
+  if (!live) return;
+  if (helper) {
+    // merge mode: the stream's spike count and pads (sub-band 0's helper)
+    if (a.merge && sb == 0) {
+      if (lane == 0) a.out_n[b] = out_base;
+      if (a.fill_pads)
+        for (int i = min(out_base, a.cap) + lane; i < a.cap; i += kWave) {
+          a.out_t[(size_t)b * a.cap + i] = kPadTime;
+          a.out_s[(size_t)b * a.cap + i] = 0;
+        }
+    }
+    return;
+  }
+  if (wl != 0) return;
+  for (int w = wv + 1; w < wv + nwps; ++w) {  // the stream's other channel-group waves
     vmin_l = min(vmin_l, red[w * 4 + 0]);
     vmax_l = max(vmax_l, red[w * 4 + 1]);
     maxcnt = max(maxcnt, red[w * 4 + 2]);
@@ -947,17 +984,11 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   const int ovf = (vmin_l < -qz.half || vmax_l > qz.half - 1) ? 1 : 0;
   if (a.merge) {
     if (lane == 0) {
-      a.out_n[b] = out_base;
       a.stats[b * 4 + 0] = vmin_l;
       a.stats[b * 4 + 1] = vmax_l;
       a.stats[b * 4 + 2] = maxcnt + 1;
       a.stats[b * 4 + 3] = ovf;
     }
-    if (a.fill_pads)
-      for (int i = min(out_base, a.cap) + lane; i < a.cap; i += kWave) {
-        a.out_t[(size_t)b * a.cap + i] = kPadTime;
-        a.out_s[(size_t)b * a.cap + i] = 0;
-      }
   } else if (lane == 0) {
     atomicMin(&a.stats[b * 4 + 0], vmin_l);
     atomicMax(&a.stats[b * 4 + 1], vmax_l);

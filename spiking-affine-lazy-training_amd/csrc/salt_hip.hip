@@ -747,7 +747,7 @@ int32_t plan_conv_mode(const salt_layer_desc* d, const salt_qparams* p, int B, b
 void choose_spw(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext,
                 ConvPlan* pl) {
   if (!pl->merge) return;
-  const int nwps = pl->ncg * pl->nsb;
+  const int nwps = pl->ncg * pl->nsb + pl->nsb;  // with the helper waves
   const char* e = getenv("SALT_CONV_SPW");
   int spw = e ? atoi(e) : 1;
   if (spw <= 1) return;
@@ -1009,7 +1009,8 @@ int32_t fill(int32_t* p, int32_t v, size_t n, hipStream_t st) {
 
 hipError_t launch_conv(const ConvArgs& a, const ConvPlan& pl, int flags, int B,
                        hipStream_t st) {
-  const dim3 grid(pl.n_rb, (B + pl.spw - 1) / pl.spw), block(kWave * pl.ncg * pl.nsb * pl.spw);
+  const dim3 grid(pl.n_rb, (B + pl.spw - 1) / pl.spw),
+      block(kWave * conv_block_waves(pl.spw, pl.ncg, pl.nsb));
   switch (pl.nit) {
 #define SALT_CASE(N) \
     case N: return launch_conv_nit##N(a, flags, grid, block, pl.lds, st);
