@@ -22,6 +22,10 @@ namespace salt {
 
 constexpr int kFcMaxWaves = 4;  // waves per stream of a directly appending FC layer
 
+// LDS of an FC work-group: the extended decay table (n_table + 2 words), padded to 16
+// bytes, then the slice's weights (WLDS) or the merge buffers.
+__host__ __device__ inline int fc_lds_table_words(int n_table) { return (n_table + 2 + 3) & ~3; }
+
 struct FcArgs {
   int n_in, n_out, words;  // words: 32-bit spike-mask words per event (sliced layers)
   Quant qz;
@@ -132,16 +136,21 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
         if (WLDS) qv[i] = (int32_t)wl[rdlane(rowv, i) + col[0]];
         else qv[i] = (int32_t)qt[(size_t)rdlane(sv, i) * a.n_out + n0 + col[0]];
       }
-      // (folding the weight into a 64-bit multiply-add shortens the chain -- 27 against
-      // 38 clock ticks per update in isolation on gfx950 -- but left this kernel's time
-      // unchanged, 0.140-0.143 ms)
+      // The lone wave of a readout is bound by its instruction count here: the decay as
+      // one 64-bit multiply-add and the extremes over pairs of events take it from about
+      // 12 to 8 instructions per update (configuration 3's readout 0.106 -> 0.095 ms).  (Folding
+      // the weight into that multiply-add as well shortens the chain -- 27 against 38
+      // clock ticks per update in isolation -- but costs an instruction: no gain.)
 #pragma unroll
-      for (int i = 0; i < kWave; ++i) {
-        const int32_t d = decay_mul<F24>(V[0], rdlane(Aj, i), fa, rc);
-        const int32_t u = (int32_t)((uint32_t)d + ((uint32_t)qv[i] << fV));
-        V[0] = fit_bits<SAT>(u, qz);
-        mn[0] = min(mn[0], u);
-        mx[0] = max(mx[0], u);
+      for (int i = 0; i < kWave; i += 2) {
+        const int32_t d0 = decay_mul_wide(V[0], rdlane(Aj, i), fa, rc);
+        const int32_t u0 = (int32_t)((uint32_t)d0 + ((uint32_t)qv[i] << fV));
+        V[0] = fit_bits<SAT>(u0, qz);
+        const int32_t d1 = decay_mul_wide(V[0], rdlane(Aj, i + 1), fa, rc);
+        const int32_t u1 = (int32_t)((uint32_t)d1 + ((uint32_t)qv[i + 1] << fV));
+        V[0] = fit_bits<SAT>(u1, qz);
+        mn[0] = min(mn[0], min(u0, u1));
+        mx[0] = max(mx[0], max(u0, u1));
       }
       return;
     }
@@ -289,18 +298,34 @@ __global__ void __launch_bounds__(kFcMaxWaves * kWave) fc_layer_kernel(FcArgs a)
   const int sw = min(kWave * NPL, a.n_out - n0);  // neurons in this slice
   const Quant& qz = a.qz;
   int32_t* ext = dyn;
-  QT* wl = reinterpret_cast<QT*>(dyn + (qz.n_table + 2));
+  // after the table, at 16 bytes (fc_lds_table_words)
+  QT* wl = reinterpret_cast<QT*>(dyn + fc_lds_table_words(qz.n_table));
   // several waves per stream (never with WLDS): per-event spike counts, two chunk
   // buffers of kFcMaxWaves x 64, then the waves' extremes
-  int32_t* merge = dyn + (qz.n_table + 2);
+  int32_t* merge = dyn + fc_lds_table_words(qz.n_table);
   int32_t* red = merge + 2 * kFcMaxWaves * kWave;
   const QT* qt = static_cast<const QT*>(a.qt);
   load_ext_table(ext, a.table, qz.n_table, qz.fa, (int)threadIdx.x, (int)blockDim.x);
-  if (WLDS)
-    for (int i = lane; i < a.n_in * sw; i += kWave) {
-      const int r = i / sw;
-      wl[i] = qt[(size_t)r * a.n_out + n0 + (i - r * sw)];
+  if (WLDS) {
+    const int n = a.n_in * sw;
+    if (sw == a.n_out && ((uintptr_t)qt & 15) == 0) {
+      // The slice is the whole layer, so its weights are one block: 16-byte copies
+      // (a readout's 15 KB in a few microseconds, against 31 element by element).
+      const int nbytes = n * (int)sizeof(QT), n16 = nbytes >> 4;
+      const uint4* s16 = reinterpret_cast<const uint4*>(qt);
+      uint4* d16 = reinterpret_cast<uint4*>(wl);
+#pragma unroll 8
+      for (int i = lane; i < n16; i += kWave) d16[i] = s16[i];
+      for (int i = (n16 << 4) + lane; i < nbytes; i += kWave)
+        reinterpret_cast<char*>(wl)[i] = reinterpret_cast<const char*>(qt)[i];
+    } else {
+      const float rsw = 1.0f / (float)sw;  // n < 2^22: the LDS holds the slice
+      for (int i = lane; i < n; i += kWave) {
+        const int r = div_small(i, sw, rsw);
+        wl[i] = qt[(size_t)r * a.n_out + n0 + (i - r * sw)];
+      }
     }
+  }
   __syncthreads();
 
   int32_t V[NPL], mn[NPL], mx[NPL], vth[NPL];

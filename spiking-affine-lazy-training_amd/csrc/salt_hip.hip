@@ -1181,7 +1181,7 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     return fail(-1, "workspace of %zu bytes below the %zu needed", workspace_bytes, need);
   const size_t sw = (size_t)std::min(kWave * pl.npl, desc->n_out);
   const size_t wbytes = (size_t)desc->n_in * sw * (prm->q_bits / 8);
-  const size_t tbytes = (size_t)(prm->n_table + 2) * 4;
+  const size_t tbytes = (size_t)fc_lds_table_words(prm->n_table) * 4;
   // the waves of a multi-wave work-group read weights from global memory (L2)
   const bool wlds = pl.wpg == 1 && wbytes + tbytes <= kFcWeightLds;
   const size_t merge = pl.wpg > 1 ? (size_t)(2 * kFcMaxWaves * kWave + 2 * kFcMaxWaves) * 4 : 0;
