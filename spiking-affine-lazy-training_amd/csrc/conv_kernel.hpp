@@ -4,10 +4,11 @@
 // A work-group owns one stream and a band of R output rows (in-kernel output: the whole
 // plane).  Its channel-group waves split that band into ncg channel groups x nsb
 // sub-bands of Rw rows; each processes, in order, the stream's events whose candidate
-// rows meet its sub-band, as decoded by the sub-band's helper wave, which also places
-// the sub-band's spikes in the output (so a channel group's wave runs nothing but its
-// events: the decode and the placement take a quarter of a stream's time when the
-// channel groups do them themselves, measured on one stream).  Everything a wave touches
+// rows meet its sub-band, as decoded by the sub-band's helper wave, which with few
+// channel groups also places the sub-band's spikes in the output (so a channel group's
+// wave runs nothing but its events: the decode and the placement take a quarter of a
+// stream's time when the channel groups do them themselves, measured on one stream);
+// with many, each channel-group wave places its own.  Everything a wave touches
 // per event lives in LDS: registers V[channel slot][position], per-position (last-update
 // time, queue count), and -- shared -- the weight codes of its channel group and the
 // extended decay table.
@@ -35,8 +36,9 @@
 // Output.  With the whole plane in the work-group, each channel-group wave stores the
 // ballot of its spikes per (chunk event, iteration) and its spike count per chunk event
 // in LDS; in the next chunk the helper wave places every group's spikes in the stream's
-// output, in the order (event, channel group, iteration, lane) = (event, ascending neuron
-// id) of salt_core/stream.py:24-46, from a scan of all the stream's waves' counts.  With
+// output (or each wave its own), in the order (event, channel group, iteration, lane) =
+// (event, ascending neuron id) of salt_core/stream.py:24-46, from a scan of all the
+// stream's waves' counts.  With
 // several work-groups per stream (state above the LDS size: bands of rows) the waves
 // stage the same ballots; in the next chunk, for each event with a spike in the band, the
 // helper stores every group's ballots as 64-bit spike words in global memory, in the
@@ -46,8 +48,8 @@
 //
 // One barrier per 64-event chunk, none inside the event loop: a wave's LDS operations
 // complete in program order, so event e+1 reads what event e wrote.  The helper decodes
-// the next chunk and places the previous one's spikes while the channel groups run this
-// one (double-buffered records and ballots).
+// the next chunk (and places or stores the previous one's spikes) while the channel
+// groups run this one (double-buffered records and ballots).
 #pragma once
 
 #include "salt_device.hpp"
@@ -96,6 +98,9 @@ struct ConvArgs {
   const int32_t* n_real;
   // outputs
   int cap, fill_pads, merge;  // merge: one work-group per stream, ordered output in-kernel
+  // merge mode: 1 = the helper waves place every channel group's spikes, 0 = each
+  // channel-group wave places its own (the helper only decodes)
+  int hwalk;
   float* out_t;
   int32_t* out_s;
   int32_t* out_n;
@@ -862,29 +867,34 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     atomicOr(&a.valid[ev], 1u << slot);
     atomicAdd(&a.seg_cnt[(size_t)b * a.nseg + jj / kCompactSeg], tot);
   };
-  // Merge mode, the helper wave of each sub-band: the sub-band's spikes of chunk k, at
+  // Merge mode: the sub-band's spikes of chunk k in channel groups [g_begin, g_end), at
   // their places in the stream's output, ordered (event, channel group, iteration, bit) =
-  // (event, ascending neuron id) -- the order of salt_core/stream.py:24-46.  Lane = the
+  // (event, ascending neuron id) -- the order of salt_core/stream.py:24-46; the helper
+  // wave places every group's (hwalk), or each channel-group wave its own.  Lane = the
   // event's index in the chunk.  An event's spikes start after those of the chunk's
   // earlier events (a scan of the stream's waves' counts) and, within it, after the lower
   // channel groups' spikes and the group's lower iterations and bits; the sub-bands'
   // ballots of one channel group are disjoint and share the lane mapping, so the bits
   // below a spike are counted in their union.
-  auto walk = [&](int k) {
+  auto walk = [&](int k, int g_begin, int g_end) {
     const int bf = k & 1;
     auto count = [&](int s2, int g2) {  // wave s2 * ncg + g2: sub-band s2, channel group g2
       return swave0[(s2 * a.ncg + g2) * lay.wave_words + lay.wcnt + bf * kWave + lane];
     };
-    int tot = 0;
+    int tot = 0, before = 0;
     for (int s2 = 0; s2 < a.nsb; ++s2)
-      for (int g2 = 0; g2 < a.ncg; ++g2) tot += count(s2, g2);
+      for (int g2 = 0; g2 < a.ncg; ++g2) {
+        const int cw = count(s2, g2);
+        tot += cw;
+        before += g2 < g_begin ? cw : 0;
+      }
     if (__ballot(tot != 0) == 0) return;  // no spike in the chunk
     const int incl = wave_incl_scan(tot);
     const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
     const int2 ev = evt0[(k % kConvEvtBufs) * kWave + lane];  // read with every lane active
     const float te = ms_time(ev.x);
-    int pos = out_base + (incl - tot);
-    for (int g2 = 0; g2 < a.ncg; ++g2) {
+    int pos = out_base + (incl - tot) + before;
+    for (int g2 = g_begin; g2 < g_end; ++g2) {
       const uint64_t* const stg_cg = reinterpret_cast<const uint64_t*>(
           swave0 + g2 * lay.wave_words + lay.stg) + bf * kWave * NIT + lane * NIT;
       const int oc0g = g2 * a.G;
@@ -929,10 +939,14 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     if (helper) {
       if (k + 1 < nchunks) decode(k + 1);
       if (k > 0) {
-        if (a.merge) walk(k - 1);
-        else if (live) store_words(k - 1);
+        if (!a.merge) {
+          if (live) store_words(k - 1);
+        } else if (a.hwalk) {
+          walk(k - 1, 0, a.ncg);
+        }
       }
     } else {
+      if (k > 0 && a.merge && !a.hwalk) walk(k - 1, cg, cg + 1);
       c.rec = recs + bf * conv_recs(PAIR);
       c.rec1 = recs1 + bf * conv_recs(PAIR);
       const int n_ev = __builtin_amdgcn_readfirstlane(nev[bf]);
@@ -943,9 +957,16 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
     }
     __syncthreads();
   }
-  if (helper && nchunks > 0) {
-    if (a.merge) walk(nchunks - 1);
-    else if (live) store_words(nchunks - 1);
+  if (nchunks > 0) {
+    if (helper) {
+      if (!a.merge) {
+        if (live) store_words(nchunks - 1);
+      } else if (a.hwalk) {
+        walk(nchunks - 1, 0, a.ncg);
+      }
+    } else if (a.merge && !a.hwalk) {
+      walk(nchunks - 1, cg, cg + 1);
+    }
   }
 
   const int T = n_eff > 0 ? time_ms(tb[n_eff - 1]) : 0;
@@ -963,19 +984,17 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   }
   __syncthreads();
   if (!live) return;
-  if (helper) {
-    // merge mode: the stream's spike count and pads (sub-band 0's helper)
-    if (a.merge && sb == 0) {
-      if (lane == 0) a.out_n[b] = out_base;
-      if (a.fill_pads)
-        for (int i = min(out_base, a.cap) + lane; i < a.cap; i += kWave) {
-          a.out_t[(size_t)b * a.cap + i] = kPadTime;
-          a.out_s[(size_t)b * a.cap + i] = 0;
-        }
-    }
-    return;
+  // merge mode: the stream's spike count and pads, by a wave that placed spikes (every
+  // such wave counts all of them): sub-band 0's helper, or the first channel group
+  if (a.merge && (a.hwalk ? helper && sb == 0 : wl == 0 && !helper)) {
+    if (lane == 0) a.out_n[b] = out_base;
+    if (a.fill_pads)
+      for (int i = min(out_base, a.cap) + lane; i < a.cap; i += kWave) {
+        a.out_t[(size_t)b * a.cap + i] = kPadTime;
+        a.out_s[(size_t)b * a.cap + i] = 0;
+      }
   }
-  if (wl != 0) return;
+  if (helper || wl != 0) return;
   for (int w = wv + 1; w < wv + nwps; ++w) {  // the stream's other channel-group waves
     vmin_l = min(vmin_l, red[w * 4 + 0]);
     vmax_l = max(vmax_l, red[w * 4 + 1]);

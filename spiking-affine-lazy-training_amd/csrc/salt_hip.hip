@@ -739,6 +739,20 @@ int32_t plan_conv_mode(const salt_layer_desc* d, const salt_qparams* p, int B, b
   return 0;
 }
 
+// Whole-plane plans: whether the helper wave places every channel group's spikes (the
+// channel groups then run nothing but their events), or each channel-group wave its own.
+// One helper keeps up with up to kConvHelperWalks (channel group, iteration) pairs: on
+// configuration 3 (3 and 2 of them) it takes conv1 0.73 -> 0.69 ms and conv2 0.64 ->
+// 0.54 ms; with 16 (configuration 2: 8 groups of two iterations) it takes twice as long
+// per chunk as the channel groups (0.71 -> 0.78 ms).  SALT_CONV_HWALK=0 / =1 forces
+// either for comparisons and tests; both give the same results.
+constexpr int kConvHelperWalks = 4;
+int helper_walks(const ConvPlan& pl) {
+  const char* e = getenv("SALT_CONV_HWALK");
+  if (e && (e[0] == '0' || e[0] == '1')) return e[0] - '0';
+  return pl.ncg * pl.nit <= kConvHelperWalks ? 1 : 0;
+}
+
 // Streams per work-group of a whole-plane plan: one unless SALT_CONV_SPW=n asks for n
 // (within 16 waves and the LDS).  Several streams per work-group advance chunk by chunk
 // together, behind one barrier; on configuration 3 that was slower than independent
@@ -1113,6 +1127,7 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     a.qz = qz; a.table = prm->d_decay_table; a.q = prm->d_q; a.q_bits = prm->q_bits;
     a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
     a.cap = out->cap; a.fill_pads = out->fill_pads; a.merge = pl.merge;
+    a.hwalk = helper_walks(pl);
     a.out_t = out->d_times; a.out_s = out->d_src; a.out_n = out->d_n;
     a.v_final = res->d_v_final; a.v_min = res->d_v_min; a.v_max = res->d_v_max;
     a.stats = res->d_stats;

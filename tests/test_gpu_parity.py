@@ -228,6 +228,41 @@ def test_conv_one_and_two_events_per_step_match_oracle(pair, monkeypatch):
         assert_layer_equal(out, ref, tag=f"pair {pair} {case} {plan} {clustered}")
 
 
+@pytest.mark.parametrize("hwalk", ["0", "1"])
+def test_conv_spikes_placed_by_the_helper_or_by_each_group_match_oracle(hwalk, monkeypatch):
+    """Whole-plane plans whose spikes the helper wave places for every channel group, or
+    each channel-group wave its own (forced through SALT_CONV_HWALK): one and two events
+    per step, one to eight channel groups, sub-bands, dense firing, a capacity cut and an
+    empty stream give the oracle's streams, registers and extremes."""
+    monkeypatch.setenv("SALT_CONV_PACKED", "0")  # the channel-slot kernel
+    monkeypatch.setenv("SALT_CONV_HWALK", hwalk)
+    cases = [((2, 34, 34, 16, 5, 2, 0, 5, 500), "0", None), ((16, 15, 15, 32, 3, 2, 0, 5, 400), "0", None),
+             ((2, 34, 34, 16, 5, 1, 0, 3, 300), "1", None), ((2, 12, 12, 8, 3, 1, 1, 5, 300), "0", "2,2"),
+             ((4, 12, 12, 40, 5, 1, 2, 3, 200), "0", None)]  # 7 groups of 3 iterations
+    for mi, (case, pair, plan) in enumerate(cases):
+        ic, h, w, oc, k, s, p, B, L = case
+        monkeypatch.setenv("SALT_CONV_PAIR", pair)
+        if plan:
+            monkeypatch.setenv("SALT_CONV_PLAN", plan)
+        else:
+            monkeypatch.delenv("SALT_CONV_PLAN", raising=False)
+        rng = np.random.default_rng(1300 + 10 * int(hwalk) + mi)
+        layer = ConvLayer(name="c", ic=ic, h_in=h, w_in=w, oc=oc, k=k, s=s, p=p, init_k=1.0,
+                          max_queue_len=L + 1,
+                          max_out_spikes=int(rng.choice([4 * L * oc, 50])))
+        params, rm = _params(rng, layer.weight_shape, layer.n_neurons, oc, MODES[mi % 5], 8,
+                             ["scalar", "channel", "neuron"][mi % 3])
+        times, src, n_real = _events(rng, B, L, ic * h * w)
+        src = _clustered_sources(rng, B, L, ic, h, w, 2 * k)
+        n_real[1] = 0  # an empty stream
+        print("hwalk", hwalk, "case", case, "pair", pair, "plan", plan, flush=True)
+        out = run_layer(layer, params, times, src, n_real, round_mode=rm)
+        geom, prm, cap = oracle_spec(layer, params, rm)
+        ref = O.layer_forward(geom, prm, times, src, n_real, cap)
+        assert int(ref["out_n"].sum()) > 0, "the case must fire"
+        assert_layer_equal(out, ref, tag=f"hwalk {hwalk} {case} {pair} {plan}")
+
+
 @pytest.mark.parametrize("pair", ["0", "1"])
 def test_conv_many_iterations_per_step_match_oracle(pair, monkeypatch):
     """One channel group per stream (SALT_CONV_PLAN=1,1) puts every channel in one wave:
