@@ -21,10 +21,10 @@ using QType = int32_t;
 
 template <int NPL, int F>
 hipError_t fc_entry(const FcArgs& a, dim3 grid, int waves, size_t lds, hipStream_t st) {
-  constexpr bool kF24 = (F & kFcF24) != 0, kSat = (F & kFcSat) != 0, kWlds = (F & kFcWlds) != 0;
+  constexpr bool kSat = (F & kFcSat) != 0, kWlds = (F & kFcWlds) != 0;
   constexpr bool kNoFire = (F & kFcNoFire) != 0;
   static bool attr_set = false;
-  auto fn = fc_layer_kernel<QType, NPL, kF24, kSat, kWlds, kNoFire>;
+  auto fn = fc_layer_kernel<QType, NPL, kSat, kWlds, kNoFire>;
   return launch_with_lds(reinterpret_cast<const void*>(fn), fn, &attr_set, grid,
                          dim3(kWave * waves), lds, st, a);
 }
@@ -45,17 +45,17 @@ hipError_t SALT_CAT(launch_fc_q, SALT_QBITS)(const FcArgs& a, int npl, int flags
                                              int waves, size_t lds, hipStream_t st) {
   // layers without a threshold (readouts) are narrow: their variant exists for slices of
   // up to 128 neurons; wider ones run the general kernel, whose thresholds never fire
-  static constexpr auto t1 = fc_table<1>(std::make_integer_sequence<int, 16>{});
-  static constexpr auto t2 = fc_table<2>(std::make_integer_sequence<int, 16>{});
-  static constexpr auto t4 = fc_table<4>(std::make_integer_sequence<int, 8>{});
-  static constexpr auto t8 = fc_table<8>(std::make_integer_sequence<int, 8>{});
-  static constexpr auto t16 = fc_table<16>(std::make_integer_sequence<int, 8>{});
+  static constexpr auto t1 = fc_table<1>(std::make_integer_sequence<int, 8>{});
+  static constexpr auto t2 = fc_table<2>(std::make_integer_sequence<int, 8>{});
+  static constexpr auto t4 = fc_table<4>(std::make_integer_sequence<int, 4>{});
+  static constexpr auto t8 = fc_table<8>(std::make_integer_sequence<int, 4>{});
+  static constexpr auto t16 = fc_table<16>(std::make_integer_sequence<int, 4>{});
   switch (npl) {
-    case 1: return t1[flags & 15](a, grid, waves, lds, st);
-    case 2: return t2[flags & 15](a, grid, waves, lds, st);
-    case 4: return t4[flags & 7](a, grid, waves, lds, st);
-    case 8: return t8[flags & 7](a, grid, waves, lds, st);
-    default: return t16[flags & 7](a, grid, waves, lds, st);
+    case 1: return t1[flags & 7](a, grid, waves, lds, st);
+    case 2: return t2[flags & 7](a, grid, waves, lds, st);
+    case 4: return t4[flags & 3](a, grid, waves, lds, st);
+    case 8: return t8[flags & 3](a, grid, waves, lds, st);
+    default: return t16[flags & 3](a, grid, waves, lds, st);
   }
 }
 

@@ -50,7 +50,7 @@ struct FcArgs {
 // The events of one chunk (one per lane of tv/sv, ne of them) with their decay codes
 // Aj.  DIRECT: the slice is the whole layer and appends spikes to the output stream;
 // otherwise it writes the chunk's spike-mask words.
-template <typename QT, int NPL, bool F24, bool SAT, bool WLDS, bool NOFIRE, bool DIRECT>
+template <typename QT, int NPL, bool SAT, bool WLDS, bool NOFIRE, bool DIRECT>
 __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const QT* qt,
                                           const int (&col)[NPL], int sw, int n0, int b,
                                           int base, int ne, int tv, int sv, int Aj,
@@ -96,10 +96,11 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
     constexpr bool LO = decltype(lo_only)::value, FV0 = decltype(fv0)::value;
 #pragma unroll
     for (int k = 0; k < NPL; ++k) {
-      // (the weight folded into a 64-bit multiply-add, (A*V + c + w*2^f_a) >> f_a, makes
-      // the register's chain shorter but measured slower: readout 0.209 -> 0.229 ms,
-      // configuration 1 0.31 -> 0.38 ms)
-      const int32_t d = decay_mul<F24>(V[k], A, fa, rc);
+      // The decay as one 64-bit multiply-add: configuration 1 0.325 -> 0.269 ms and 5
+      // 35.2 -> 32.5 ms against the split 24-bit form.  (Folding the weight into it too,
+      // (A*V + c + w*2^f_a) >> f_a, shortens the chain but costs an instruction:
+      // measured slower.)
+      const int32_t d = decay_mul_wide(V[k], A, fa, rc);
       const uint32_t qw = FV0 ? (uint32_t)(int32_t)qc[k] : ((uint32_t)(int32_t)qc[k] << fV);
       const int32_t u = (int32_t)((uint32_t)d + qw);
       const int32_t f = fit_bits<SAT>(u, qz);
@@ -138,9 +139,9 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
       }
       // The lone wave of a readout is bound by its instruction count here: the decay as
       // one 64-bit multiply-add and the extremes over pairs of events take it from about
-      // 12 to 8 instructions per update (configuration 3's readout 0.106 -> 0.095 ms).  (Folding
-      // the weight into that multiply-add as well shortens the chain -- 27 against 38
-      // clock ticks per update in isolation -- but costs an instruction: no gain.)
+      // 12 to 8 instructions per update (configuration 3's readout 0.106 -> 0.095 ms).
+      // (Folding the weight into that multiply-add as well shortens the chain -- 27
+      // against 38 clock ticks per update in isolation -- but costs an instruction.)
 #pragma unroll
       for (int i = 0; i < kWave; i += 2) {
         const int32_t d0 = decay_mul_wide(V[0], rdlane(Aj, i), fa, rc);
@@ -288,7 +289,7 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
 
 // NOFIRE: the layer has no threshold (v_th None: a readout), so nothing fires, no spike
 // is staged or placed, and the register's chain per event ends at the write-back.
-template <typename QT, int NPL, bool F24, bool SAT, bool WLDS, bool NOFIRE = false>
+template <typename QT, int NPL, bool SAT, bool WLDS, bool NOFIRE = false>
 __global__ void __launch_bounds__(kFcMaxWaves * kWave) fc_layer_kernel(FcArgs a) {
   extern __shared__ int32_t dyn[];
   const int lane = threadIdx.x & (kWave - 1);
@@ -376,11 +377,11 @@ __global__ void __launch_bounds__(kFcMaxWaves * kWave) fc_layer_kernel(FcArgs a)
     const int Aj = ext[decay_slot(tv - tp, ntab)];
     t_prev = rdlane(tv, ne - 1);
     if (a.direct)
-      fc_events<QT, NPL, F24, SAT, WLDS, NOFIRE, true>(a, wl, qt, col, sw, n0, b, base, ne, tv,
+      fc_events<QT, NPL, SAT, WLDS, NOFIRE, true>(a, wl, qt, col, sw, n0, b, base, ne, tv,
                                                        sv, Aj,
                                                V, mn, mx, vth, out_base, merge);
     else
-      fc_events<QT, NPL, F24, SAT, WLDS, NOFIRE, false>(a, wl, qt, col, sw, n0, b, base, ne, tv,
+      fc_events<QT, NPL, SAT, WLDS, NOFIRE, false>(a, wl, qt, col, sw, n0, b, base, ne, tv,
                                                         sv,
                                                 Aj, V, mn, mx, vth, out_base, merge);
   }

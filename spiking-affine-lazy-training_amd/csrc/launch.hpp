@@ -40,8 +40,8 @@ constexpr int kPackFlagCombos = 16;
 SALT_PACK_IMAXES(SALT_DECLARE_PACK)
 #undef SALT_DECLARE_PACK
 
-// FC flags: bit 2 = 24-bit high multiply, bit 1 = saturate, bit 0 = weights in LDS.
-enum : int { kFcNoFire = 8, kFcF24 = 4, kFcSat = 2, kFcWlds = 1 };
+// FC flags: bit 2 = no threshold (a readout), bit 1 = saturate, bit 0 = weights in LDS.
+enum : int { kFcNoFire = 4, kFcSat = 2, kFcWlds = 1 };
 
 #define SALT_DECLARE_FC(B)                                                             \
   hipError_t launch_fc_q##B(const FcArgs& a, int npl, int flags, dim3 grid, int waves, \

@@ -47,6 +47,7 @@ struct Quant {
 // split multiply of salt_core/quant/fixed_point.py:47-65 (bit-identical to
 // (A*V + c) >> f_a with an exact product).  A < 2^15 and the low part < 2^15, so the
 // low product is a 24-bit unsigned multiply-add; F24: the high part fits 24 bits too.
+// (The trace kernel's form; the layer kernels use decay_mul_wide.)
 template <bool F24>
 __device__ __forceinline__ int32_t decay_mul(int32_t v, int32_t a, int fa, int rc) {
   const int32_t hi = v >> fa;
@@ -58,8 +59,8 @@ __device__ __forceinline__ int32_t decay_mul(int32_t v, int32_t a, int fa, int r
 // The same value as one 64-bit multiply-add: V*A = hi*A*2^f_a + lo*A, so
 // (V*A + c) >> f_a = hi*A + ((lo*A + c) >> f_a) exactly; |V| < 2^29 and A <= 2^f_a keep
 // the product in 64 bits and the result in 32.  Two instructions on gfx950
-// (v_mad_i64_i32, v_alignbit_b32) against six for the split form, which pays off in the
-// conv loop; the FC loop's chain is faster with the split form.
+// (v_mad_i64_i32 and a 64-bit shift) against six for the split form, which pays off in
+// every layer loop (measured on MI355X: conv, the firing FC and the readout).
 __device__ __forceinline__ int32_t decay_mul_wide(int32_t v, int32_t a, int fa, int rc) {
   return (int32_t)(((int64_t)v * a + rc) >> fa);
 }

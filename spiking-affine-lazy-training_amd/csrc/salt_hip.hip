@@ -1100,7 +1100,6 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     return fail(-1, "give both or neither of v_min/v_max");
   const bool ext = res->d_v_min != nullptr;
   const Quant qz = make_quant(prm);
-  const bool f24 = (prm->i_V + prm->f_V - prm->f_a) <= 24;
   const bool sat = prm->overflow_mode == SALT_SATURATE;
 
   if (desc->kind == SALT_LAYER_CONV) {
@@ -1213,7 +1212,7 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
   a.stats = res->d_stats;
   a.masks = static_cast<uint32_t*>(d_workspace);
   if (!pl.direct && (rc = fill(res->d_stats, 0, (size_t)B * 4, st))) return rc;
-  const int flags = (f24 ? kFcF24 : 0) | (sat ? kFcSat : 0) | (wlds ? kFcWlds : 0) |
+  const int flags = (sat ? kFcSat : 0) | (wlds ? kFcWlds : 0) |
                     (prm->v_th_kind == SALT_VTH_NONE ? kFcNoFire : 0);
   const dim3 grid(pl.n_slices, B);
   switch (prm->q_bits) {
