@@ -665,11 +665,16 @@ int32_t plan_conv_mode(const salt_layer_desc* d, const salt_qparams* p, int B, b
 
 // Chooses between steps of one event and steps of two (a half-wave each, for events
 // whose candidate blocks are disjoint; candidates must fit 32 lanes).  Pairs shorten a
-// stream's chain of steps by up to half -- 20% less time for the heaviest conv1 stream
-// of configuration 3 -- but, with as many waves per stream, do more work per event (the
-// steps with one event leave half a wave idle) and need more LDS; measured on MI355X
-// they win while the grid has fewer than two work-groups per compute unit (B <= 384 on
-// configuration 3) and lose when it fills the chip (B = 1024).
+// stream's chain of steps -- a lone conv1 stream of configuration 3 0.38 -> 0.32 ms --
+// but, with more waves per stream, do more work per event (the steps with one event
+// leave half a wave idle), so they pay only while the chip has room for those waves.
+// Measured on MI355X (configuration 3, its first B streams, one-event / two-event
+// steps): conv1 at B = 256 0.47 / 0.42 ms, at 384 0.50 / 0.57; conv2 (five waves per
+// two-event stream against seven for conv1) at 384 0.49 / 0.43, at 512 0.52 / 0.52;
+// configuration 2 (nine waves per two-event stream, B = 256) 0.67 / 0.69.  The rule
+// that fits them: two-event steps while their plan puts at most kPairWavesPerCu waves on
+// a compute unit.
+constexpr long kPairWavesPerCu = 8;
 int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool ext,
                   bool notrunc, ConvPlan* pl) {
   const int NC = (d->k - 1) / std::max(d->s, 1) + 1;
@@ -677,7 +682,8 @@ int32_t plan_conv(const salt_layer_desc* d, const salt_qparams* p, int B, bool e
   if (NC * NC <= kWave / 2 && force != 0) {
     const int32_t rc = plan_conv_mode(d, p, B, ext, notrunc, true, pl);
     if (rc) return rc;
-    if (force == 1 || (long)B * pl->n_rb < 2L * device_cus()) return 0;
+    const long waves = (long)B * pl->n_rb * conv_block_waves(pl->spw, pl->ncg, pl->nsb);
+    if (force == 1 || waves <= kPairWavesPerCu * device_cus()) return 0;
   }
   return plan_conv_mode(d, p, B, ext, notrunc, false, pl);
 }
@@ -743,10 +749,11 @@ int32_t plan_conv_mode(const salt_layer_desc* d, const salt_qparams* p, int B, b
 // channel groups then run nothing but their events), or each channel-group wave its own.
 // One helper keeps up with up to kConvHelperWalks (channel group, iteration) pairs: on
 // configuration 3 (3 and 2 of them) it takes conv1 0.73 -> 0.69 ms and conv2 0.64 ->
-// 0.54 ms; with 16 (configuration 2: 8 groups of two iterations) it takes twice as long
-// per chunk as the channel groups (0.71 -> 0.78 ms).  SALT_CONV_HWALK=0 / =1 forces
-// either for comparisons and tests; both give the same results.
-constexpr int kConvHelperWalks = 4;
+// 0.54 ms, on configuration 2 with steps of one event (8) 0.666 -> 0.659 ms; with 16
+// (configuration 2 with steps of two events: 8 groups of two iterations) it takes twice
+// as long per chunk as the channel groups (0.71 -> 0.78 ms).  SALT_CONV_HWALK=0 / =1
+// forces either for comparisons and tests; both give the same results.
+constexpr int kConvHelperWalks = 8;
 int helper_walks(const ConvPlan& pl) {
   const char* e = getenv("SALT_CONV_HWALK");
   if (e && (e[0] == '0' || e[0] == '1')) return e[0] - '0';
