@@ -246,10 +246,11 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
         const int te_bits = __float_as_int(ms_time(tv));
         char* const otb = reinterpret_cast<char*>(ot);
         char* const osb = reinterpret_cast<char*>(os);
-        const uint64_t lane_bit = 1ull << lane;
         auto place = [&](int e, int at, auto check) {
           constexpr bool kCheck = decltype(check)::value;
-          const float te = __int_as_float(__builtin_amdgcn_readlane(te_bits, e));
+          // the event's time in a VGPR once, not moved there again for every store
+          float te = __int_as_float(__builtin_amdgcn_readlane(te_bits, e));
+          asm volatile("" : "+v"(te));
 #pragma unroll
           for (int k = 0; k < NPL; ++k) {
             const uint64_t m =
@@ -257,7 +258,9 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)sp[k], e);
             const uint32_t r = (uint32_t)at + __builtin_amdgcn_mbcnt_hi(
                                    (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            if ((m & lane_bit) && (!kCheck || (int)r < room)) {
+            // The lane's own bit of the uniform mask: the mask itself becomes the
+            // execution mask (no per-lane shift, and or compare).
+            if (__builtin_amdgcn_inverse_ballot_w64(m) && (!kCheck || (int)r < room)) {
               *reinterpret_cast<float*>(otb + (r << 2)) = te;
               *reinterpret_cast<int32_t*>(osb + (r << 2)) = n0 + k * kWave + lane;
             }
