@@ -863,14 +863,14 @@ struct FcPlan {
 };
 
 // Waves per stream of a directly appending FC layer: SALT_FC_WAVES=n (1..kFcMaxWaves)
-// for tuning runs and tests, else 2.  Measured on MI355X: configuration 1 (128 neurons,
+// for tuning runs and tests, else 4.  Measured on MI355X: configuration 1 (128 neurons,
 // one stream) 0.42 -> 0.30 ms with two waves of 64 instead of one of 128; configuration 5
-// (1024 neurons, 4096 streams, ~180 spikes per event) 61.9 ms with one wave of 1024 or
-// two of 512, 70.3 ms with four of 256 -- its time is set by the L2 requests of the
-// spike stores (one cache line per lane), which more waves only contend for.
+// (1024 neurons, 4096 streams, ~180 spikes per event, dense chunks placed with one run
+// of entries per store) 31.0-32.4 ms with two waves of 512, 24.0-25.1 ms with four of
+// 256, 29.8-30.7 ms with eight of 128 (a build allowing eight).
 int fc_waves_limit() {
   const char* e = getenv("SALT_FC_WAVES");
-  const int n = e ? atoi(e) : 2;
+  const int n = e ? atoi(e) : 4;
   return std::max(1, std::min(n, kFcMaxWaves));
 }
 
