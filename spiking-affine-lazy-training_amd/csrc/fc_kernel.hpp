@@ -79,8 +79,27 @@ __device__ __forceinline__ void fc_events(const FcArgs& a, const QT* wl, const Q
       for (int k = 0; k < NPL; ++k) q[k] = wl[row + col[k]];
     } else {
       const int s_e = rdlane(sv, ec);
+      if constexpr (NPL >= 4) {
+        // Wide slices: the row base in scalar registers and a 32-bit lane offset, so the
+        // load takes the scalar-base form and no 64-bit multiply-add runs per event (the
+        // empty asms keep the base scalar and the offset 32-bit; address space 1 keeps
+        // the load global): configuration 5 24.4 -> 22.7 ms.  A lone wave (configuration
+        // 1) pays for the scalar chain readlane -> multiply -> add on every event
+        // instead: 0.231 -> 0.297 ms, so narrow slices keep the vector form.
+        typedef const __attribute__((address_space(1))) char gchar;
+        typedef const __attribute__((address_space(1))) QT gqt;
+        gchar* rowb = (gchar*)(qt + ((size_t)s_e * a.n_out + n0));
+        asm volatile("" : "+s"(rowb));
 #pragma unroll
-      for (int k = 0; k < NPL; ++k) q[k] = qt[(size_t)s_e * a.n_out + n0 + col[k]];
+        for (int k = 0; k < NPL; ++k) {
+          uint32_t ob = (uint32_t)col[k] * (uint32_t)sizeof(QT);
+          asm volatile("" : "+v"(ob));
+          q[k] = *(gqt*)(rowb + ob);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < NPL; ++k) q[k] = qt[(size_t)s_e * a.n_out + n0 + col[k]];
+      }
     }
   };
   // DIRECT: lane e of klo/khi[k] collects event e's ballot of the neurons that kept their
@@ -299,7 +318,10 @@ template <typename QT, int NPL, bool SAT, bool WLDS, bool NOFIRE = false>
 __global__ void __launch_bounds__(kFcMaxWaves * kWave) fc_layer_kernel(FcArgs a) {
   extern __shared__ int32_t dyn[];
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = (int)(threadIdx.x / kWave), wpg = (int)(blockDim.x / kWave);
+  // wide slices: the wave index (so n0) provably uniform, for the scalar weight-row base
+  const int wave = NPL >= 4 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave))
+                            : (int)(threadIdx.x / kWave);
+  const int wpg = (int)(blockDim.x / kWave);
   const int b = blockIdx.y;
   const int n0 = (blockIdx.x * wpg + wave) * (kWave * NPL);
   const int sw = min(kWave * NPL, a.n_out - n0);  // neurons in this slice
