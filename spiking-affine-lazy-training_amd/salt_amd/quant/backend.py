@@ -63,8 +63,12 @@ def _to_numpy(x) -> np.ndarray:
 
 
 def _as_int32(x) -> np.ndarray:
-    """Integer array -> int32 with two's-complement wrap, as jnp.asarray(..., int32) does."""
-    return _to_numpy(x).astype(np.int64).astype(np.int32)
+    """Integer array -> int32 with two's-complement wrap, as jnp.asarray(..., int32) does.
+    An int32 array is returned as it is (no copy: weight tables can be gigabytes)."""
+    a = _to_numpy(x)
+    if a.dtype == np.int32:
+        return a
+    return a.astype(np.int64).astype(np.int32)
 
 
 class DeviceLayerParams(NamedTuple):
@@ -87,7 +91,7 @@ def _code_bits(q: np.ndarray) -> tuple[np.ndarray, int]:
         return q.astype(np.int8), 8
     if -32768 <= lo and hi <= 32767:
         return q.astype(np.int16), 16
-    return q.astype(np.int32), 32
+    return q.astype(np.int32, copy=False), 32
 
 
 def prepare_params(layer, params: QuantizedLayerParams, device: torch.device) -> DeviceLayerParams:
