@@ -106,3 +106,25 @@ def test_reference_truncation_keeps_neuron_major_prefix():
     assert s[0].tolist() == [0, 1, 0] and t[0].tolist() == [1.0, 2.0, 3.0]
     t, s = reference_truncation(times, src, np.array([5]), 6, 3)
     assert s[0].tolist() == [2, 0, 2, 1, 0, 0] and t[0, 5] == np.float32(1e12)
+
+
+def test_weight_codes_wrap_to_int32_and_int32_tables_are_not_copied():
+    """q → int32 with two's-complement wrap, as jnp.asarray(q, jnp.int32) gives
+    (salt_core/quant/backend.py:14-20 takes the codes as int32); an int32 table is used as
+    it is, and its narrowest code width is chosen from its range."""
+    from salt_amd.quant.backend import _as_int32, _code_bits
+    q64 = np.array([2 ** 31, -2 ** 31 - 1, 2 ** 32 + 5, -7, 127], np.int64)
+    np.testing.assert_array_equal(_as_int32(q64), np.array([-2 ** 31, 2 ** 31 - 1, 5, -7, 127]))
+    assert _as_int32(q64).dtype == np.int32
+    qu = np.array([255, 128, 0], np.uint8)
+    np.testing.assert_array_equal(_as_int32(qu), [255, 128, 0])
+    q32 = np.arange(-5, 5, dtype=np.int32).reshape(2, 5)
+    assert _as_int32(q32) is q32
+    codes, bits = _code_bits(q32)
+    assert bits == 8 and codes.dtype == np.int8
+    np.testing.assert_array_equal(codes, q32)
+    wide = np.array([[70000, -3]], np.int32)
+    codes, bits = _code_bits(wide)
+    assert bits == 32 and np.shares_memory(codes, wide)
+    codes, bits = _code_bits(np.array([[-32768, 32767]], np.int32))
+    assert bits == 16 and codes.dtype == np.int16
