@@ -101,6 +101,8 @@ struct ConvArgs {
   // merge mode: 1 = the helper waves place every channel group's spikes, 0 = each
   // channel-group wave places its own (the helper only decodes)
   int hwalk;
+  // 1: the helper waves run at issue priority 1 (their per-chunk work is heavy), 0: at 0
+  int hprio;
   float* out_t;
   int32_t* out_s;
   int32_t* out_n;
@@ -934,6 +936,9 @@ __global__ void __launch_bounds__(kWave * kConvBlockWaves) conv_layer_kernel(Con
   // finished before it; the walk of chunk k-1 reads the ballots and counts written
   // before it (the channel groups write chunk k's into the other buffers meanwhile), and
   // event info decoded two chunks before the next decode's.
+  // A helper with heavy per-chunk work is served before the channel-group waves at their
+  // lowest priority, so its stream does not wait for it at the chunk barrier.
+  if (helper && a.hprio) __builtin_amdgcn_s_setprio(1);
   for (int k = 0; k < nchunks; ++k) {
     const int bf = k & 1;
     if (helper) {

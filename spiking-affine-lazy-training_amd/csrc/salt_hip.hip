@@ -760,6 +760,20 @@ int helper_walks(const ConvPlan& pl) {
   return pl.ncg * pl.nit <= kConvHelperWalks ? 1 : 0;
 }
 
+// Issue priority of the helper waves: 1 where their per-chunk work is heavy -- placing
+// the spikes of kConvHelperPrioWalks or more (channel group, iteration) pairs, or storing
+// a row band's spike words -- else 0, below the channel-group waves for most of each
+// chunk.  Measured on MI355X (priority 0 / 1): configuration 2 (8 pairs) 0.660-0.663 /
+// 0.624-0.637 ms, configuration 4 (row bands) 2.257 / 2.242-2.250 ms; configuration 3's
+// conv2 (2 pairs) 0.546-0.548 / 0.550-0.552 ms, conv1 (3 pairs) unchanged.  Steps of two
+// events keep 0 (not measured there).
+constexpr int kConvHelperPrioWalks = 4;
+int helper_priority(const ConvPlan& pl, int hwalk) {
+  if (pl.pair) return 0;
+  if (!pl.merge) return 1;
+  return hwalk && pl.ncg * pl.nit >= kConvHelperPrioWalks ? 1 : 0;
+}
+
 // Streams per work-group of a whole-plane plan: one unless SALT_CONV_SPW=n asks for n
 // (within 16 waves and the LDS).  Several streams per work-group advance chunk by chunk
 // together, behind one barrier; on configuration 3 that was slower than independent
@@ -1134,6 +1148,7 @@ int32_t layer_forward(const salt_layer_desc* desc, const salt_qparams* prm,
     a.L = L; a.times = in->d_times; a.src = in->d_src; a.n_real = in->d_n_real;
     a.cap = out->cap; a.fill_pads = out->fill_pads; a.merge = pl.merge;
     a.hwalk = helper_walks(pl);
+    a.hprio = helper_priority(pl, a.hwalk);
     a.out_t = out->d_times; a.out_s = out->d_src; a.out_n = out->d_n;
     a.v_final = res->d_v_final; a.v_min = res->d_v_min; a.v_max = res->d_v_max;
     a.stats = res->d_stats;
